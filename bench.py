@@ -1,0 +1,296 @@
+"""Benchmark of the FP8 block-scaled GEMM hot path on one MI355X.
+
+Default workload: dense fp8_gemm_nt at M = 4096 over
+the DeepSeek-V3 (N, K) sweep {(2112,7168), (24576,1536), (7168,16384),
+(4096,7168), (7168,2048)}, e4m3 operands with 1x128 / 128x128 FP32 scales, BF16
+output. One step = one call per shape (5 launches). `value` is total
+algorithmic FLOPs / wall time of the timed steps (inputs resident in HBM).
+
+Other workloads (`--workload`): dense_acc (FP32 C += A.B^T), contiguous
+(config 3, 8 experts, 32768 tokens), masked (config 4, 16 experts, max_m 256),
+fp8fp4 (config 5).
+
+Prints one JSON line. `roofline` is computed from per-launch durations measured
+live with HIP events on the launch stream; `cpu_baseline` times the CPU FP32
+dequantize-then-matmul reference (oracle/) on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, 'deepgemm-amd_amd'))
+
+PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA (AMD public spec: 2.5 PFLOP/s bf16 x2)
+PEAK_FP4_TFLOPS = 10100.0
+PEAK_HBM_GBS = 8000.0
+DENSE_NK = [(2112, 7168), (24576, 1536), (7168, 16384), (4096, 7168), (7168, 2048)]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--workload', default='dense',
+                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4'])
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--cpu-sample-m', type=int, default=512)
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- workloads
+
+class Launch:
+    """One GEMM launch of the workload with its algorithmic FLOPs and bytes."""
+
+    def __init__(self, name, fn, flops, nbytes):
+        self.name, self.fn, self.flops, self.nbytes = name, fn, flops, nbytes
+
+
+def _quant_a(m, k, gen, dev):
+    import torch
+    import deep_gemm
+    x = torch.randn((m, k), generator=gen).bfloat16().to(dev)
+    return deep_gemm.per_token_cast_to_fp8(x, use_ue8m0=False)
+
+
+def _quant_b(n, k, gen, dev):
+    import torch
+    import deep_gemm
+    x = torch.randn((n, k), generator=gen).bfloat16().to(dev)
+    return deep_gemm.per_block_cast_to_fp8(x, use_ue8m0=False)
+
+
+def make_dense(acc: bool):
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator().manual_seed(0)
+    m = 4096
+    launches = []
+    for n, k in DENSE_NK:
+        a = _quant_a(m, k, gen, dev)
+        b = _quant_b(n, k, gen, dev)
+        if acc:
+            d = (torch.randn((m, n), generator=gen) * 32).to(dev)
+            fn = (lambda a=a, b=b, d=d: deep_gemm.fp8_gemm_nt(a, b, d, c=d))
+            out_bytes = 8 * m * n
+        else:
+            d = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            fn = (lambda a=a, b=b, d=d: deep_gemm.fp8_gemm_nt(a, b, d))
+            out_bytes = 2 * m * n
+        nbytes = m * k + n * k + 4 * m * ((k + 127) // 128) + 4 * ((n + 127) // 128) * ((k + 127) // 128) + out_bytes
+        launches.append(Launch(f'n{n}_k{k}', fn, 2 * m * n * k, nbytes))
+    cfg = {'workload': 'fp8_gemm_nt M=4096 DeepSeek-V3 (N,K) sweep' + (' FP32 C-accumulate' if acc else ''),
+           'm': m, 'nk': DENSE_NK, 'out': 'f32 (D=C+AB^T)' if acc else 'bf16',
+           'recipe': '1x128 A / 128x128 B FP32 scales'}
+    return launches, cfg, 'mfma'
+
+
+def make_contiguous():
+    import numpy as np
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator().manual_seed(0)
+    rng = np.random.default_rng(0)
+    g, total = 8, 32768
+    ms = rng.multinomial(total, rng.dirichlet(np.ones(g)))
+    align = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    aligned = [(int(x) + align - 1) // align * align for x in ms]
+    m_pad = sum(aligned)
+    idx = torch.full((m_pad,), -1, dtype=torch.int32)
+    s = 0
+    for i, (mi, ai) in enumerate(zip(ms, aligned)):
+        idx[s:s + int(mi)] = i
+        s += ai
+    idx = idx.to(dev)
+    launches = []
+    for n, k in [(4096, 7168), (7168, 2048)]:
+        x = torch.randn((m_pad, k), generator=gen).bfloat16()
+        x[idx.cpu() < 0] = 0
+        a = deep_gemm.per_token_cast_to_fp8(x.to(dev), use_ue8m0=False)
+        bq = torch.empty((g, n, k), dtype=torch.float8_e4m3fn, device=dev)
+        bs = torch.empty((g, (n + 127) // 128, (k + 127) // 128), device=dev)
+        for i in range(g):
+            bq[i], bs[i] = _quant_b(n, k, gen, dev)
+        d = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
+        fn = (lambda a=a, b=(bq, bs), d=d: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, idx))
+        nbytes = m_pad * k + g * n * k + 2 * m_pad * n + 4 * m_pad * ((k + 127) // 128) + 4 * m_pad
+        launches.append(Launch(f'n{n}_k{k}', fn, 2 * total * n * k, nbytes))
+    cfg = {'workload': 'm_grouped_fp8_gemm_nt_contiguous 8 experts 32768 tokens Dirichlet(1)',
+           'tokens_per_expert': [int(v) for v in ms], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)]}
+    return launches, cfg, 'mfma'
+
+
+def make_masked():
+    import numpy as np
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator().manual_seed(0)
+    rng = np.random.default_rng(0)
+    g, max_m = 16, 256
+    masked = rng.integers(96, 161, size=g).astype(np.int32)
+    mm = torch.from_numpy(masked).to(dev)
+    sum_m = int(masked.sum())
+    launches = []
+    for n, k in [(4096, 7168), (7168, 2048)]:
+        aq = torch.empty((g, max_m, k), dtype=torch.float8_e4m3fn, device=dev)
+        as_ = torch.empty((g, max_m, (k + 127) // 128), device=dev)
+        bq = torch.empty((g, n, k), dtype=torch.float8_e4m3fn, device=dev)
+        bs = torch.empty((g, (n + 127) // 128, (k + 127) // 128), device=dev)
+        for i in range(g):
+            aq[i], as_[i] = _quant_a(max_m, k, gen, dev)
+            as_[i, int(masked[i]):] = 0
+            bq[i], bs[i] = _quant_b(n, k, gen, dev)
+        d = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
+        fn = (lambda a=(aq, as_), b=(bq, bs), d=d: deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, 128))
+        nbytes = g * n * k + sum_m * k + 2 * sum_m * n + 4 * sum_m * ((k + 127) // 128) + \
+            4 * g * ((n + 127) // 128) * ((k + 127) // 128)
+        launches.append(Launch(f'n{n}_k{k}', fn, 2 * sum_m * n * k, nbytes))
+    cfg = {'workload': 'm_grouped_fp8_gemm_nt_masked 16 experts max_m=256 masked_m~U[96,160]',
+           'masked_m': masked.tolist(), 'nk': [(4096, 7168), (7168, 2048)]}
+    return launches, cfg, 'hbm'
+
+
+def make_fp8fp4():
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator().manual_seed(0)
+    m, n, k = 4096, 7168, 7168
+    a = deep_gemm.per_token_cast_to_fp8(torch.randn((m, k), generator=gen).bfloat16().to(dev), use_ue8m0=True)
+    b = deep_gemm.per_token_cast_to_fp4(torch.randn((n, k), generator=gen).bfloat16().to(dev), use_ue8m0=True,
+                                        gran_k=32)
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    fn = (lambda: deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, 128), recipe_b=(1, 32)))
+    nbytes = m * k + n * k // 2 + 4 * m * (k // 128) + 4 * n * (k // 32) + 2 * m * n
+    cfg = {'workload': 'fp8_fp4_gemm_nt M=4096 N=K=7168, A e4m3 1x128 UE8M0, B e2m1 1x32 UE8M0', 'm': m, 'n': n,
+           'k': k}
+    return [Launch('m4096_n7168_k7168', fn, 2 * m * n * k, nbytes)], cfg, 'mfma'
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(workload: str, sample_m: int):
+    """Time the oracle's FP32 dequantize-then-matmul on the host (bounded sample)."""
+    import numpy as np
+    import torch
+    from oracle import gemm as ogemm, quant as oquant
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else os.cpu_count()
+    rng = np.random.default_rng(0)
+    nk = DENSE_NK if workload in ('dense', 'dense_acc') else [(4096, 7168), (7168, 2048)]
+    flops, secs = 0, 0.0
+    for n, k in nk:
+        a = torch.randn((sample_m, k), generator=torch.Generator().manual_seed(1)).bfloat16().float().numpy()
+        b = torch.randn((n, k), generator=torch.Generator().manual_seed(2)).bfloat16().float().numpy()
+        qa, sfa = oquant.per_token_cast_to_fp8(a, use_ue8m0=False)
+        qb, sfb = oquant.per_block_cast_to_fp8(b, use_ue8m0=False)
+        t0 = time.perf_counter()
+        ogemm.gemm_nt_f32(oquant.dequant_per_token(qa, sfa), oquant.dequant_per_block(qb, sfb))
+        secs += time.perf_counter() - t0
+        flops += 2 * sample_m * n * k
+    del rng
+    return {'value': round(flops / secs / 1e12, 4), 'unit': 'TFLOPS', 'cores': cores, 'kind': 'port',
+            'sample': f'M={sample_m} rows of each (N,K) shape of the workload: FP32 dequantize (numpy) + '
+                      f'FP32 matmul (numpy BLAS, {cores} host threads), one pass, {secs:.1f} s total'}
+
+
+# ---------------------------------------------------------------- main
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only: this build has no multi-GPU path '
+              f'(requested --gpus {args.gpus}); run with --gpus 1', file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import deep_gemm
+    torch.cuda.set_device(0)
+    makers = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
+              'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4}
+    launches, cfg, bound = makers[args.workload]()
+    torch.cuda.synchronize()
+    log(f'workload {args.workload}: {len(launches)} launches per step')
+
+    for _ in range(args.warmup):
+        for l in launches:
+            l.fn()
+    torch.cuda.synchronize()
+
+    # Per-launch durations, HIP events on the launch stream (torch's current stream,
+    # which the library launches on), back-to-back repetitions of each launch.
+    stream = torch.cuda.current_stream()
+    per = []
+    for l in launches:
+        reps = max(5, args.steps)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            l.fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        per.append(us)
+        log(f'  {l.name}: {us:8.1f} us  {l.flops / us / 1e6:7.1f} TFLOPS  {l.nbytes / us / 1e3:7.1f} GB/s  '
+            f'[{deep_gemm.get_last_config()}]')
+
+    # Whole-job timed region: K steps, synchronized on both sides.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for l in launches:
+            l.fn()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    total_flops = sum(l.flops for l in launches) * args.steps
+    total_bytes = sum(l.nbytes for l in launches)
+    value = total_flops / elapsed / 1e12
+
+    kernel_us = sum(per)
+    if bound == 'mfma':
+        peak = PEAK_FP8_TFLOPS
+        achieved = sum(l.flops for l in launches) / kernel_us / 1e6
+        unit = 'TFLOP/s'
+    else:
+        peak = PEAK_HBM_GBS
+        achieved = total_bytes / kernel_us / 1e3
+        unit = 'GB/s'
+    roofline = {'bound': bound, 'achieved': round(achieved, 2), 'peak': peak, 'unit': unit,
+                'frac': round(achieved / peak, 4), 'traffic': None,
+                'kernel': 'fp8_gemm_1d2d_kernel' if args.workload != 'fp8fp4' else 'fp8_fp4_gemm_kernel',
+                'per_launch_us': {l.name: round(u, 2) for l, u in zip(launches, per)},
+                'per_launch_tflops': {l.name: round(l.flops / u / 1e6, 1) for l, u in zip(launches, per)},
+                'per_launch_gbs': {l.name: round(l.nbytes / u / 1e3, 1) for l, u in zip(launches, per)}}
+    out = {
+        'metric': 'FP8 block-scaled GEMM TFLOPS + % of MI355X FP8 MFMA peak, DSV3 shapes',
+        'value': round(value, 2),
+        'unit': 'TFLOPS',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(elapsed / args.steps * 1e3, 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'e4m3 (fp32 accumulate)' if args.workload != 'fp8fp4' else 'e4m3 x e2m1 (fp32 accumulate)',
+        'data': 'synthetic (seeded randn, bf16 -> quantized)',
+        'config': cfg,
+        'roofline': roofline,
+    }
+    if not args.no_cpu_baseline:
+        log('cpu baseline ...')
+        out['cpu_baseline'] = cpu_baseline(args.workload, args.cpu_sample_m)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

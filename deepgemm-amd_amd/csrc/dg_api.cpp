@@ -1,0 +1,697 @@
+// C-ABI entry points: argument validation, recipe resolution and dispatch.
+//
+// Each dg_* function mirrors one registered API of the reference pybind module
+// and runs the reference's checks in the same order:
+//   - major / shape / dtype checks: csrc/utils/layout.hpp:17-82
+//   - early_return (empty problems, K == 0, C vs D): csrc/apis/gemm.hpp:17-53
+//   - recipe and SF layout checks: csrc/apis/layout.hpp:11-87,
+//     csrc/utils/layout.hpp:84-140
+//   - the three GEMMs: csrc/apis/gemm.hpp:78-133, 181-250, 269-318
+// Failures raise dgm::Error, converted at the boundary into a status code and
+// the thread-local message returned by dg_last_error().
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "dg_internal.hpp"
+
+namespace dgm {
+namespace {
+
+thread_local std::string t_last_error;
+thread_local std::string t_last_config;
+
+// Process-wide knobs (the reference keeps them in lazily created singletons,
+// csrc/runtime/runtime.hpp:104, csrc/jit_kernels/heuristics/runtime.hpp:67).
+constexpr int kDefaultMKAlignment = 128;
+std::atomic<int> g_num_sms{0};                 // 0: query the device
+std::atomic<int> g_mk_alignment{kDefaultMKAlignment};
+std::atomic<int> g_tile_m{0}, g_tile_n{0};     // 0: heuristic
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        t_last_error.clear();
+        return DG_OK;
+    } catch (const Error& e) {
+        t_last_error = e.what();
+        return e.code();
+    } catch (const std::exception& e) {
+        t_last_error = std::string("Internal error: ") + e.what();
+        return DG_ERR_INTERNAL;
+    } catch (...) {
+        t_last_error = "Internal error: unknown exception";
+        return DG_ERR_INTERNAL;
+    }
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+int elem_size(int dtype) {
+    switch (dtype) {
+        case DG_F32: case DG_I32: return 4;
+        case DG_BF16: case DG_F16: return 2;
+        case DG_E4M3: case DG_I8: case DG_U8: return 1;
+        case DG_I64: return 8;
+        default: return 0;
+    }
+}
+
+// Light view over dg_tensor with Python-style negative indices.
+struct View {
+    const dg_tensor* t;
+    int dim() const { return t->ndim; }
+    int64_t size(int i) const { return t->sizes[i < 0 ? i + t->ndim : i]; }
+    int64_t stride(int i) const { return t->strides[i < 0 ? i + t->ndim : i]; }
+    int dtype() const { return t->dtype; }
+    const void* data() const { return t->data; }
+    bool on_device() const { return t->device >= 0; }
+};
+
+View view(const dg_tensor* t, const char* name) {
+    if (t == nullptr) throw Error(DG_ERR_INVALID, "Assertion", __FILE__, __LINE__, std::string(name) + " != nullptr");
+    DG_CHECK(t->ndim >= 0 && t->ndim <= 4);
+    DG_CHECK(elem_size(t->dtype) > 0);
+    return View{t};
+}
+
+// csrc/utils/layout.hpp:18-27
+void major_check(const View& t) {
+    DG_CHECK(t.dim() == 2 || t.dim() == 3);
+    if (t.dim() == 3) DG_CHECK(t.stride(0) == t.size(-2) * t.size(-1));
+    DG_CHECK(t.stride(-2) == 1 || t.stride(-1) == 1);
+}
+
+// csrc/utils/layout.hpp:29-33: true = K-major
+bool is_k_major(const View& t) {
+    major_check(t);
+    return t.stride(-1) == 1;
+}
+
+// csrc/utils/layout.hpp:35-40
+void check_major_type_cd(const View& t) {
+    major_check(t);
+    DG_CHECK(t.stride(-1) == 1);
+}
+
+// csrc/utils/layout.hpp:48-55 (the device check replaces is_cuda)
+void check_shape(const View& t, int n) {
+    DG_CHECK(t.on_device());
+    DG_CHECK(t.dim() == n);
+}
+
+bool is_fp4(const View& t) { return t.dtype() == DG_I8; }
+
+// csrc/utils/layout.hpp:66-73: (mn, logical k); packed FP4 doubles K.
+std::pair<int64_t, int64_t> check_ab(const View& t) {
+    check_shape(t, 2);
+    int64_t mn = t.size(0), k = t.size(1);
+    if (t.dtype() != DG_E4M3) {
+        DG_CHECK(t.dtype() == DG_I8);
+        k *= 2;
+    }
+    return {mn, k};
+}
+
+// csrc/utils/layout.hpp:75-82
+void check_grouped_ab(const View& t, int64_t& g, int64_t& mn, int64_t& k) {
+    check_shape(t, 3);
+    g = t.size(0), mn = t.size(1), k = t.size(2);
+    if (t.dtype() != DG_E4M3) {
+        DG_CHECK(t.dtype() == DG_I8);
+        k *= 2;
+    }
+}
+
+// Alignment rules of the gfx950 kernels: operand rows are read as 16-byte
+// vectors and D rows written as 8/16-byte vectors. The reference imposes the
+// same 16-byte rule through its TMA descriptors (runtime_utils.hpp:119-159).
+void check_vector_alignment(const View& t, const char* what) {
+    const auto addr = reinterpret_cast<uintptr_t>(t.data());
+    const int64_t row_bytes = t.stride(-2) * elem_size(t.dtype());
+    if (addr % 16 != 0 || (t.size(-2) > 1 && row_bytes % 16 != 0) ||
+        (t.dim() == 3 && t.size(0) > 1 && (t.stride(0) * elem_size(t.dtype())) % 16 != 0))
+        throw Error(DG_ERR_INVALID, "Assertion", __FILE__, __LINE__,
+                    std::string(what) + ": base address and row pitch must be 16-byte aligned");
+}
+
+struct Recipe {
+    int gran_mn_a, gran_k_a, gran_mn_b, gran_k_b;
+};
+
+// csrc/utils/layout.hpp:84-98 for this device: FP32 SFB -> (1, 128, 128),
+// packed UE8M0 SFB -> (1, 1, 128).
+void default_recipe(const View& sfa, const View& sfb, int out[3]) {
+    DG_CHECK(sfb.dtype() == DG_F32 || sfb.dtype() == DG_I32);
+    (void)sfa;
+    out[0] = 1;
+    out[1] = sfb.dtype() == DG_F32 ? 128 : 1;
+    out[2] = 128;
+}
+
+// csrc/apis/layout.hpp:60-87 (pair resolution)
+Recipe resolve_recipe(const dg_recipe* r, const View& sfa, const View& sfb) {
+    dg_recipe rr{};
+    if (r) rr = *r;
+    if (!rr.has_recipe_ab && !rr.has_recipe) {
+        default_recipe(sfa, sfb, rr.recipe);
+        rr.has_recipe = 1;
+    }
+    DG_CHECK((rr.has_recipe_ab != 0) != (rr.has_recipe != 0));
+    Recipe out{};
+    if (rr.has_recipe) {
+        out = {rr.recipe[0], rr.recipe[2], rr.recipe[1], rr.recipe[2]};
+    } else {
+        out = {rr.recipe_a[0], rr.recipe_a[1], rr.recipe_b[0], rr.recipe_b[1]};
+    }
+    DG_CHECK(out.gran_mn_a > 0 && out.gran_k_a > 0 && out.gran_mn_b > 0 && out.gran_k_b > 0);
+    return out;
+}
+
+// csrc/utils/layout.hpp:100-140 (shape part): SF [(G,) ceil(mn/gran_mn), ceil(k/(gran_k*(4 if int)))]
+void check_sf_layout(const View& sf, int64_t mn, int64_t k, int gran_mn, int gran_k, int64_t num_groups) {
+    DG_CHECK(sf.dtype() == DG_F32 || sf.dtype() == DG_I32);
+    DG_CHECK(sf.on_device());
+    DG_CHECK(sf.dim() == (num_groups >= 0 ? 3 : 2));
+    if (num_groups >= 0) DG_CHECK(sf.size(-3) == num_groups);
+    DG_CHECK(sf.size(-2) == ceil_div(mn, gran_mn));
+    DG_CHECK(sf.size(-1) == ceil_div(k, (int64_t)gran_k * (sf.dtype() == DG_F32 ? 1 : 4)));
+}
+
+// Packed-UE8M0 layout requirement (csrc/utils/layout.hpp:121-130): MN-major words.
+void check_packed_sf_strides(const View& sf, int64_t mn) {
+    DG_CHECK(sf.stride(-2) == 1 || mn == 1);
+    DG_CHECK(sf.stride(-1) >= align_up(mn, 4));
+}
+
+int num_sms_now() {
+    int v = g_num_sms.load();
+    if (v > 0) return v;
+    int dev = 0;
+    DG_HIP_CHECK(hipGetDevice(&dev));
+    DG_HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+    return v;
+}
+
+// ---------------------------------------------------------------- early return
+
+// csrc/apis/gemm.hpp:17-53. Returns true when the call is fully handled.
+// Unlike the reference, a C that differs from D is not copied into D first:
+// the kernels read C and write D directly (D = C + A.B^T in the epilogue).
+bool early_return(int64_t m, int64_t n, int64_t k, const View& d, const dg_tensor* c, hipStream_t stream) {
+    if (m == 0 || n == 0) return true;
+    bool same = false;
+    if (c) {
+        const View cv = view(c, "c");
+        same = cv.data() == d.data();
+        if (same) {
+            DG_CHECK(cv.dim() == d.dim());
+            for (int i = 0; i < d.dim(); ++i) DG_CHECK(cv.size(i) == d.size(i) && cv.stride(i) == d.stride(i));
+        }
+    }
+    DG_CHECK(d.dtype() == DG_BF16 || d.dtype() == DG_F32 || d.dtype() == DG_E4M3);
+    // An FP8 D needs an SFD output, which these entry points do not take (gemm.hpp:31).
+    DG_CHECK(d.dtype() != DG_E4M3);
+    if (c) {
+        const View cv = view(c, "c");
+        check_major_type_cd(cv);
+        DG_CHECK(d.dtype() == cv.dtype());
+        DG_CHECK(cv.on_device());
+        DG_CHECK(cv.dim() == d.dim());
+        for (int i = 0; i < d.dim(); ++i) DG_CHECK(cv.size(i) == d.size(i));
+    }
+    if (k == 0) {
+        if (!same) {
+            const View cv = c ? view(c, "c") : d;
+            launch_fill_or_copy(const_cast<void*>(d.data()), c ? cv.data() : nullptr, (int)m, (int)n, 1, d.stride(-2),
+                                0, c ? cv.stride(-2) : 0, 0, elem_size(d.dtype()), stream);
+        }
+        return true;
+    }
+    return false;
+}
+
+// ---------------------------------------------------------------- heuristics
+
+const char* kind_name(GemmKind k) {
+    switch (k) {
+        case kNormal: return "normal";
+        case kContiguous: return "m_grouped_contiguous";
+        case kMasked: return "m_grouped_masked";
+        case kPsum: return "m_grouped_contiguous_psum";
+    }
+    return "?";
+}
+
+// Tile choice for the FP32-scale kernel. A tile shape's cost is the number of
+// rounds of resident workgroups it needs times the work of one tile divided
+// by that shape's relative MFMA efficiency (larger tiles re-read less LDS per
+// MFMA). Grouped kinds need block_m to divide the row alignment.
+TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t groups, int align_m) {
+    const int tm = g_tile_m.load(), tn = g_tile_n.load();
+    if (tm > 0 && tn > 0) {
+        if (!fp8_1d2d_tile_supported(tm, tn)) DG_UNSUPPORTED("tile override not compiled");
+        if ((kind == kContiguous || kind == kPsum) && align_m % tm != 0)
+            DG_UNSUPPORTED("tile override block_m must divide the M alignment");
+        return {tm, tn};
+    }
+    struct Cand { int bm, bn, per_cu; double eff; };
+    static const Cand cands[] = {{128, 128, 2, 1.00}, {128, 64, 3, 0.80}, {64, 128, 3, 0.80}, {64, 64, 4, 0.62}};
+    int cus = 256;
+    try { cus = num_sms_now(); } catch (const Error&) {}
+    double best = 1e300;
+    TileConfig out{64, 64};
+    for (const auto& c : cands) {
+        if ((kind == kContiguous || kind == kPsum) && align_m % c.bm != 0) continue;
+        const int64_t tiles = ceil_div(m_rows, c.bm) * ceil_div(n, c.bn) * groups;
+        const int64_t slots = (int64_t)cus * c.per_cu;
+        const double rounds = (double)ceil_div(tiles, slots);
+        const double cost = rounds * c.bm * c.bn / c.eff / c.per_cu;
+        if (cost < best - 1e-9) best = cost, out = {c.bm, c.bn};
+    }
+    return out;
+}
+
+void record_config(const char* kernel, GemmKind kind, const TileConfig& t, int64_t m, int64_t n, int64_t k,
+                   int64_t g) {
+    char buf[256];
+    std::snprintf(buf, sizeof(buf), "%s kind=%s block_m=%d block_n=%d m=%lld n=%lld k=%lld groups=%lld", kernel,
+                  kind_name(kind), t.block_m, t.block_n, (long long)m, (long long)n, (long long)k, (long long)g);
+    t_last_config = buf;
+}
+
+// ---------------------------------------------------------------- dispatch
+
+struct Operands {
+    View a, sfa, b, sfb, d;
+    const dg_tensor* c;
+    const dg_tensor* layout;
+};
+
+// FP32 SF recipe of the reference's SM90 "1D2D" kernel:
+// A 1 x 128 per token, B 128 x 128 per block, both e4m3.
+bool is_1d2d(const Operands& o, const Recipe& r) {
+    return o.a.dtype() == DG_E4M3 && o.b.dtype() == DG_E4M3 && o.sfa.dtype() == DG_F32 &&
+           o.sfb.dtype() == DG_F32 && r.gran_mn_a == 1 && r.gran_k_a == 128 && r.gran_mn_b == 128 &&
+           r.gran_k_b == 128;
+}
+
+bool is_ue8m0_path(const Operands& o, const Recipe& r) {
+    const bool fp4 = is_fp4(o.a) || is_fp4(o.b);
+    const bool packed = o.sfa.dtype() == DG_I32 || o.sfb.dtype() == DG_I32;
+    const bool gran_ok = (r.gran_k_a == 32 || r.gran_k_a == 128) && (r.gran_k_b == 32 || r.gran_k_b == 128) &&
+                         r.gran_mn_a == 1 && (r.gran_mn_b == 1 || (r.gran_mn_b == 128 && o.sfb.dtype() == DG_F32));
+    return gran_ok && (fp4 || packed || r.gran_k_a == 32 || r.gran_k_b == 32);
+}
+
+void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int64_t n, int64_t k, int64_t groups,
+              int disable_ue8m0_cast, int zero_padding, hipStream_t stream) {
+    const int align_m = g_mk_alignment.load();
+    const bool grouped_b = kind != kNormal;
+    const bool grouped_a = kind == kMasked;
+
+    if (is_1d2d(o, r)) {
+        check_vector_alignment(o.a, "a");
+        check_vector_alignment(o.b, "b");
+        check_vector_alignment(o.d, "d");
+        if (o.c) check_vector_alignment(view(o.c, "c"), "c");
+        Fp8GemmArgs args{};
+        args.a = static_cast<const uint8_t*>(o.a.data());
+        args.b = static_cast<const uint8_t*>(o.b.data());
+        args.sfa = static_cast<const float*>(o.sfa.data());
+        args.sfb = static_cast<const float*>(o.sfb.data());
+        args.d = const_cast<void*>(o.d.data());
+        args.c = o.c ? o.c->data : nullptr;
+        args.layout = o.layout ? static_cast<const int32_t*>(o.layout->data) : nullptr;
+        args.m = (int32_t)m, args.n = (int32_t)n, args.k = (int32_t)k;
+        args.num_groups = (int32_t)groups;
+        args.out_f32 = o.d.dtype() == DG_F32;
+        args.align_m = align_m;
+        args.zero_padding = zero_padding;
+        args.lda = o.a.stride(-2), args.ldb = o.b.stride(-2), args.ldd = o.d.stride(-2);
+        args.ldc = o.c ? o.c->strides[o.c->ndim - 2] : 0;
+        args.a_gs = grouped_a ? o.a.stride(0) : 0;
+        args.b_gs = grouped_b ? o.b.stride(0) : 0;
+        args.d_gs = grouped_a ? o.d.stride(0) : 0;
+        args.c_gs = 0;
+        args.sfa_sm = o.sfa.stride(-2), args.sfa_sk = o.sfa.stride(-1);
+        args.sfa_gs = grouped_a ? o.sfa.stride(0) : 0;
+        args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
+        args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
+        const int64_t m_rows = m;
+        const TileConfig t = choose_tile_1d2d(kind, m_rows, n, kind == kMasked ? groups : 1, align_m);
+        if ((kind == kContiguous || kind == kPsum) && align_m % t.block_m != 0)
+            DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
+        record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
+        launch_fp8_gemm_1d2d(kind, t, args, stream);
+        return;
+    }
+
+    if (is_ue8m0_path(o, r)) {
+        // csrc/apis/layout.hpp:46-47: FP32 SFs are cast to UE8M0 on this path.
+        if (o.sfa.dtype() == DG_F32 || o.sfb.dtype() == DG_F32) DG_CHECK(!disable_ue8m0_cast);
+        if (o.sfa.dtype() == DG_I32) check_packed_sf_strides(o.sfa, m);
+        if (o.sfb.dtype() == DG_I32) check_packed_sf_strides(o.sfb, n);
+        check_vector_alignment(o.a, "a");
+        check_vector_alignment(o.b, "b");
+        check_vector_alignment(o.d, "d");
+        if (o.c) check_vector_alignment(view(o.c, "c"), "c");
+        Fp8Fp4GemmArgs args{};
+        args.a = static_cast<const uint8_t*>(o.a.data());
+        args.b = static_cast<const uint8_t*>(o.b.data());
+        args.sfa = o.sfa.data();
+        args.sfb = o.sfb.data();
+        args.d = const_cast<void*>(o.d.data());
+        args.c = o.c ? o.c->data : nullptr;
+        args.layout = o.layout ? static_cast<const int32_t*>(o.layout->data) : nullptr;
+        args.m = (int32_t)m, args.n = (int32_t)n, args.k = (int32_t)k;
+        args.num_groups = (int32_t)groups;
+        args.out_f32 = o.d.dtype() == DG_F32;
+        args.align_m = align_m;
+        args.zero_padding = zero_padding;
+        args.a_fp4 = is_fp4(o.a), args.b_fp4 = is_fp4(o.b);
+        args.sfa_packed = o.sfa.dtype() == DG_I32, args.sfb_packed = o.sfb.dtype() == DG_I32;
+        args.gran_k_a = r.gran_k_a, args.gran_k_b = r.gran_k_b;
+        args.lda = o.a.stride(-2), args.ldb = o.b.stride(-2), args.ldd = o.d.stride(-2);
+        args.ldc = o.c ? o.c->strides[o.c->ndim - 2] : 0;
+        args.a_gs = grouped_a ? o.a.stride(0) : 0;
+        args.b_gs = grouped_b ? o.b.stride(0) : 0;
+        args.d_gs = grouped_a ? o.d.stride(0) : 0;
+        args.c_gs = 0;
+        // gran_mn_b == 128 with FP32 SFB: the row index is n / 128 (the reference
+        // broadcasts rows before packing, csrc/apis/layout.hpp:48-49).
+        args.sfa_sm = o.sfa.stride(-2), args.sfa_sk = o.sfa.stride(-1);
+        args.sfa_gs = grouped_a ? o.sfa.stride(0) : 0;
+        args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
+        args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
+        args.sfb_row_shift = r.gran_mn_b == 128 ? 7 : 0;
+        const TileConfig t{128, 128};
+        if ((kind == kContiguous || kind == kPsum) && align_m % t.block_m != 0)
+            DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 128 on the UE8M0 path");
+        record_config("fp8_fp4_gemm_ue8m0", kind, t, m, n, k, groups);
+        launch_fp8_fp4_gemm(kind, t, args, stream);
+        return;
+    }
+
+    if (o.sfa.dtype() == DG_F32 && o.sfb.dtype() == DG_F32 && r.gran_mn_b == 1)
+        DG_UNSUPPORTED("FP32-scale 1D1D recipe (gran_n == 1, reference sm90_fp8_gemm_1d1d) is not provided");
+    DG_UNSUPPORTED("Unsupported architecture or scaling factor types");
+}
+
+// ---------------------------------------------------------------- the three GEMMs
+
+void gemm_nt_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
+                  const dg_tensor* d_, const dg_tensor* c, const dg_recipe* recipe, int disable_ue8m0_cast,
+                  hipStream_t stream) {
+    const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
+               d = view(d_, "d");
+    // Shape must be [M, K] @ [N, K].T; the gfx950 kernels need K-major operands
+    // (as the reference's SM90 path does, csrc/apis/gemm.hpp:93-97).
+    DG_CHECK(is_k_major(a));
+    DG_CHECK(is_k_major(b));
+    check_major_type_cd(d);
+    const auto [m, k] = check_ab(a);
+    const auto [n, k_] = check_ab(b);
+    check_shape(d, 2);
+    const int64_t m_ = d.size(0), n_ = d.size(1);
+    DG_CHECK(m == m_ && n == n_ && k == k_);
+    DG_CHECK(d.dtype() == DG_BF16 || d.dtype() == DG_F32);
+    if (early_return(m, n, k, d, c, stream)) return;
+    const Recipe r = resolve_recipe(recipe, sfa, sfb);
+    check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, -1);
+    check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, -1);
+    run_gemm(kNormal, Operands{a, sfa, b, sfb, d, c, nullptr}, r, m, n, k, 1, disable_ue8m0_cast, 0, stream);
+}
+
+void contiguous_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
+                     const dg_tensor* d_, const dg_tensor* layout_, const dg_recipe* recipe, int disable_ue8m0_cast,
+                     int use_psum_layout, int ensure_zero_padding, int expected_m_for_psum_layout,
+                     hipStream_t stream) {
+    const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
+               d = view(d_, "d"), gl = view(layout_, "grouped_layout");
+    // Shape must be [M, K] @ [G, N, K].mT (csrc/apis/gemm.hpp:195-218)
+    DG_CHECK(is_k_major(a));
+    DG_CHECK(is_k_major(b));
+    DG_CHECK(gl.dim() == 1 && (gl.size(0) <= 1 || gl.stride(0) == 1));
+    const auto [m, k] = check_ab(a);
+    int64_t groups, n, k_;
+    check_grouped_ab(b, groups, n, k_);
+    check_shape(d, 2);
+    const int64_t m_ = d.size(0), n_ = d.size(1);
+    DG_CHECK(m == m_ && n == n_ && k == k_);
+    DG_CHECK(n > 0 && k > 0 && groups > 0);
+    DG_CHECK(d.dtype() == DG_BF16);
+    DG_CHECK(gl.dtype() == DG_I32);
+    check_shape(gl, 1);
+    if (use_psum_layout) {
+        DG_CHECK(gl.size(0) == groups);
+    } else {
+        DG_CHECK(gl.size(0) == m);
+        DG_CHECK(expected_m_for_psum_layout < 0);
+    }
+    check_major_type_cd(d);
+    if (m == 0) return;
+    const Recipe r = resolve_recipe(recipe, sfa, sfb);
+    check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, -1);
+    check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, groups);
+    run_gemm(use_psum_layout ? kPsum : kContiguous, Operands{a, sfa, b, sfb, d, nullptr, layout_}, r, m, n, k, groups,
+             disable_ue8m0_cast, use_psum_layout && ensure_zero_padding, stream);
+}
+
+void masked_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
+                 const dg_tensor* d_, const dg_tensor* masked_m_, int expected_m, const dg_recipe* recipe,
+                 int disable_ue8m0_cast, hipStream_t stream) {
+    const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
+               d = view(d_, "d"), mm = view(masked_m_, "masked_m");
+    // Shape must be [G, M, K] @ [G, N, K].mT (csrc/apis/gemm.hpp:282-297)
+    DG_CHECK(is_k_major(a) && is_k_major(b));
+    DG_CHECK(mm.dim() == 1 && (mm.size(0) <= 1 || mm.stride(0) == 1));
+    int64_t g, m, k, g_, n, k_;
+    check_grouped_ab(a, g, m, k);
+    check_grouped_ab(b, g_, n, k_);
+    check_shape(d, 3);
+    const int64_t g__ = d.size(0), m_ = d.size(1), n_ = d.size(2);
+    const int64_t g___ = mm.size(0);
+    DG_CHECK(g == g_ && g == g__ && g == g___);
+    DG_CHECK(m == m_ && n == n_ && k == k_);
+    DG_CHECK(expected_m > 0 && m > 0 && n > 0 && k > 0 && g > 0);
+    DG_CHECK(d.dtype() == DG_BF16);
+    DG_CHECK(mm.dtype() == DG_I32);
+    DG_CHECK(mm.on_device());
+    check_major_type_cd(d);
+    const Recipe r = resolve_recipe(recipe, sfa, sfb);
+    check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, g);
+    check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, g);
+    run_gemm(kMasked, Operands{a, sfa, b, sfb, d, nullptr, masked_m_}, r, m, n, k, g, disable_ue8m0_cast, 0, stream);
+}
+
+// ---------------------------------------------------------------- SF layouts
+
+// csrc/apis/layout.hpp:11-58 (planning half).
+int plan_sf(const dg_tensor* sf_, int32_t mn, int32_t k, const int32_t* recipe3, const int32_t* recipe2,
+            int32_t num_groups, int32_t is_sfa, int32_t disable_ue8m0_cast) {
+    const View sf = view(sf_, "sf");
+    int gran_mn, gran_k;
+    if (recipe3) {
+        DG_CHECK(is_sfa == 0 || is_sfa == 1);
+        gran_mn = is_sfa ? recipe3[0] : recipe3[1];
+        gran_k = recipe3[2];
+    } else if (recipe2) {
+        DG_CHECK(is_sfa < 0);
+        gran_mn = recipe2[0];
+        gran_k = recipe2[1];
+    } else {
+        DG_UNSUPPORTED("Invalid recipe");
+    }
+    check_sf_layout(sf, mn, k, gran_mn, gran_k, num_groups);
+    // (FP32, 1, 128): MN-major TMA-aligned copy, as the reference's SM90 path.
+    if (sf.dtype() == DG_F32 && gran_mn == 1 && gran_k == 128) return 1;
+    // (FP32, 128, 128): used as is (reference checks contiguity, layout.hpp:132-138).
+    if (sf.dtype() == DG_F32 && gran_mn == 128 && gran_k == 128) {
+        if (num_groups >= 0) DG_CHECK(sf.stride(-3) == sf.size(-2) * sf.size(-1));
+        DG_CHECK((sf.stride(-1) == 1 && sf.stride(-2) == sf.size(-1)) ||
+                 (sf.stride(-1) == sf.size(-2) && sf.stride(-2) == 1));
+        return 0;
+    }
+    // (FP32, x, 32): UE8M0 pack (the reference's SM100 path, layout.hpp:45-51).
+    if (sf.dtype() == DG_F32 && gran_k == 32) {
+        DG_CHECK(!disable_ue8m0_cast);
+        return 2;
+    }
+    // (INT, 1, 32/128): already packed; check TMA-aligned MN-major strides.
+    if (sf.dtype() == DG_I32 && gran_mn == 1 && (gran_k == 32 || gran_k == 128)) {
+        if (num_groups >= 0) DG_CHECK(sf.stride(-3) == sf.stride(-1) * sf.size(-1));
+        check_packed_sf_strides(sf, mn);
+        DG_CHECK(sf.stride(-1) % 4 == 0);
+        return 0;
+    }
+    DG_UNSUPPORTED("Unknown SF transformation");
+}
+
+void sf3(const View& v, int64_t& g, int64_t& mn, int64_t& k, int64_t& sg, int64_t& smn, int64_t& sk) {
+    DG_CHECK(v.dim() == 2 || v.dim() == 3);
+    g = v.dim() == 3 ? v.size(0) : 1;
+    sg = v.dim() == 3 ? v.stride(0) : 0;
+    mn = v.size(-2), k = v.size(-1), smn = v.stride(-2), sk = v.stride(-1);
+}
+
+void transpose_impl(const dg_tensor* sf_, const dg_tensor* out_, hipStream_t stream) {
+    const View sf = view(sf_, "sf"), out = view(out_, "out");
+    DG_CHECK(sf.dtype() == DG_F32 && out.dtype() == DG_F32);
+    DG_CHECK(sf.on_device() && out.on_device());
+    int64_t g, mn, k, sg, smn, sk, g2, mn2, k2, og, omn, ok;
+    sf3(sf, g, mn, k, sg, smn, sk);
+    sf3(out, g2, mn2, k2, og, omn, ok);
+    DG_CHECK(g == g2 && mn == mn2 && k == k2);
+    const int64_t amn = align_up(mn, 4);
+    DG_CHECK(omn == 1 && ok == amn);
+    if (g > 1) DG_CHECK(og == amn * k);
+    SfTransposeArgs args{static_cast<const float*>(sf.data()), static_cast<float*>(const_cast<void*>(out.data())),
+                         (int32_t)g, (int32_t)mn, (int32_t)k, sg, smn, sk, og, ok};
+    launch_sf_transpose(args, stream);
+}
+
+void pack_impl(const dg_tensor* sf_, const dg_tensor* out_, hipStream_t stream) {
+    const View sf = view(sf_, "sf"), out = view(out_, "out");
+    DG_CHECK(sf.dtype() == DG_F32 && out.dtype() == DG_I32);
+    DG_CHECK(sf.on_device() && out.on_device());
+    int64_t g, mn, k, sg, smn, sk, g2, mn2, pk, og, omn, ok;
+    sf3(sf, g, mn, k, sg, smn, sk);
+    sf3(out, g2, mn2, pk, og, omn, ok);
+    DG_CHECK(g == g2 && mn == mn2 && pk == ceil_div(k, 4));
+    const int64_t amn = align_up(mn, 4);
+    DG_CHECK(omn == 1 && ok == amn);
+    if (g > 1) DG_CHECK(og == amn * pk);
+    SfPackArgs args{static_cast<const float*>(sf.data()), static_cast<int32_t*>(const_cast<void*>(out.data())),
+                    (int32_t)g, (int32_t)mn, (int32_t)k, (int32_t)pk, sg, smn, sk, og, ok};
+    launch_sf_pack_ue8m0(args, stream);
+}
+
+}  // namespace
+}  // namespace dgm
+
+using namespace dgm;
+
+extern "C" {
+
+const char* dg_last_error(void) { return t_last_error.c_str(); }
+
+const char* dg_version(void) { return "deepgemm-mi355x 0.1 (gfx950; DeepGEMM 2.8.1 FP8 GEMM API)"; }
+
+int dg_init(void) {
+    return guarded([] {
+        g_num_sms = 0;
+        g_mk_alignment = kDefaultMKAlignment;
+        g_tile_m = 0;
+        g_tile_n = 0;
+    });
+}
+
+int dg_shutdown(void) { return guarded([] {}); }
+
+int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b, const dg_tensor* sfb,
+                       const dg_tensor* d, const dg_tensor* c, const dg_recipe* recipe, int32_t disable_ue8m0_cast,
+                       void* stream) {
+    return guarded([&] {
+        gemm_nt_impl(a, sfa, b, sfb, d, c, recipe, disable_ue8m0_cast, static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_m_grouped_fp8_fp4_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
+                                            const dg_tensor* sfb, const dg_tensor* d, const dg_tensor* grouped_layout,
+                                            const dg_recipe* recipe, int32_t disable_ue8m0_cast,
+                                            int32_t use_psum_layout, int32_t ensure_zero_padding,
+                                            int32_t expected_m_for_psum_layout, void* stream) {
+    return guarded([&] {
+        contiguous_impl(a, sfa, b, sfb, d, grouped_layout, recipe, disable_ue8m0_cast, use_psum_layout,
+                        ensure_zero_padding, expected_m_for_psum_layout, static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
+                                        const dg_tensor* sfb, const dg_tensor* d, const dg_tensor* masked_m,
+                                        int32_t expected_m, const dg_recipe* recipe, int32_t disable_ue8m0_cast,
+                                        void* stream) {
+    return guarded([&] {
+        masked_impl(a, sfa, b, sfb, d, masked_m, expected_m, recipe, disable_ue8m0_cast,
+                    static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_get_tma_aligned_size(int32_t x, int32_t element_size, int32_t* out) {
+    return guarded([&] {
+        DG_CHECK(out != nullptr);
+        DG_CHECK(element_size > 0 && 16 % element_size == 0);
+        *out = (int32_t)align_up(x, 16 / element_size);
+    });
+}
+
+int dg_get_mn_major_tma_aligned_tensor(const dg_tensor* sf, const dg_tensor* out, void* stream) {
+    return guarded([&] { transpose_impl(sf, out, static_cast<hipStream_t>(stream)); });
+}
+
+int dg_get_mn_major_tma_aligned_packed_ue8m0_tensor(const dg_tensor* sf, const dg_tensor* out, void* stream) {
+    return guarded([&] { pack_impl(sf, out, static_cast<hipStream_t>(stream)); });
+}
+
+int dg_plan_sf_transform(const dg_tensor* sf, int32_t mn, int32_t k, const int32_t* recipe3, const int32_t* recipe2,
+                         int32_t num_groups, int32_t is_sfa, int32_t disable_ue8m0_cast, int32_t* kind) {
+    return guarded([&] {
+        DG_CHECK(kind != nullptr);
+        *kind = plan_sf(sf, mn, k, recipe3, recipe2, num_groups, is_sfa, disable_ue8m0_cast);
+    });
+}
+
+int dg_set_num_sms(int32_t num_sms) {
+    return guarded([&] {
+        DG_CHECK(num_sms > 0);
+        g_num_sms = num_sms;
+    });
+}
+
+int dg_get_num_sms(int32_t* out) {
+    return guarded([&] {
+        DG_CHECK(out != nullptr);
+        *out = num_sms_now();
+    });
+}
+
+int dg_set_mk_alignment_for_contiguous_layout(int32_t alignment) {
+    return guarded([&] {
+        DG_CHECK(alignment > 0);
+        g_mk_alignment = alignment;
+    });
+}
+
+int32_t dg_get_mk_alignment_for_contiguous_layout(void) { return g_mk_alignment.load(); }
+
+int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m) {
+    // The gfx950 kernels use M blocks of at most 128 rows; 128 keeps every
+    // compiled block_m a divisor (csrc/jit_kernels/heuristics/runtime.hpp:57-64).
+    (void)expected_m;
+    return kDefaultMKAlignment;
+}
+
+int dg_set_tile_override(int32_t block_m, int32_t block_n) {
+    return guarded([&] {
+        if (block_m == 0 && block_n == 0) {
+            g_tile_m = 0, g_tile_n = 0;
+            return;
+        }
+        if (!fp8_1d2d_tile_supported(block_m, block_n)) DG_UNSUPPORTED("tile shape not compiled");
+        g_tile_m = block_m, g_tile_n = block_n;
+    });
+}
+
+int dg_last_config(char* buf, int32_t cap) {
+    return guarded([&] {
+        DG_CHECK(buf != nullptr && cap > 0);
+        std::snprintf(buf, (size_t)cap, "%s", t_last_config.c_str());
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// Internal declarations shared by the host API (dg_api.cpp) and the HIP
+// launchers (dg_gemm_*.hip, dg_layout.hip). Not part of the public ABI.
+#pragma once
+
+#include <cstdint>
+#include <exception>
+#include <string>
+
+#include <hip/hip_runtime_api.h>
+
+#include "deepgemm_mi355x.h"
+
+namespace dgm {
+
+// Host-side error carried to the C-ABI boundary, where it becomes a status code
+// plus the thread-local dg_last_error() string. The message format follows the
+// reference's DGException (csrc/utils/exception.hpp:17-19).
+class Error final : public std::exception {
+public:
+    Error(int code, const char* kind, const char* file, int line, const std::string& what)
+        : code_(code) {
+        const char* base = file;
+        for (const char* p = file; *p; ++p)
+            if (*p == '/') base = p + 1;
+        msg_ = std::string(kind) + " error (" + base + ":" + std::to_string(line) + "): " + what;
+    }
+    const char* what() const noexcept override { return msg_.c_str(); }
+    int code() const { return code_; }
+
+private:
+    int code_;
+    std::string msg_;
+};
+
+#define DG_CHECK(cond)                                                                     \
+    do {                                                                                   \
+        if (!(cond)) throw ::dgm::Error(DG_ERR_INVALID, "Assertion", __FILE__, __LINE__, #cond); \
+    } while (0)
+
+#define DG_UNSUPPORTED(reason) \
+    throw ::dgm::Error(DG_ERR_UNSUPPORTED, "Unsupported", __FILE__, __LINE__, (reason))
+
+#define DG_HIP_CHECK(cmd)                                                                   \
+    do {                                                                                    \
+        hipError_t e_ = (cmd);                                                              \
+        if (e_ != hipSuccess)                                                               \
+            throw ::dgm::Error(DG_ERR_HIP, "HIP", __FILE__, __LINE__,                       \
+                               std::string(#cmd) + ": " + hipGetErrorString(e_));           \
+    } while (0)
+
+// Which rows of A/D an M-block covers and how the block finds its B group.
+enum GemmKind : int {
+    kNormal = 0,       // dense: one B
+    kContiguous = 1,   // m_indices [M]: expert of block = max(0, m_indices[block start])
+    kMasked = 2,       // masked_m [G]: A/D are [G, max_m, *]
+    kPsum = 3,         // psum ends [G]: group i rows [align(end[i-1]), end[i])
+};
+
+// Arguments of the FP32-scale ("1D2D": 1x128 A scales, 128x128 B scales) kernel.
+// All strides are in elements. Pointers are device addresses.
+struct Fp8GemmArgs {
+    const uint8_t* a;          // e4m3
+    const uint8_t* b;          // e4m3
+    const float* sfa;
+    const float* sfb;
+    void* d;                   // bf16 or f32
+    const void* c;             // same dtype as d, or null
+    const int32_t* layout;     // m_indices / masked_m / psum ends, or null
+    int32_t m, n, k;           // m: rows of A (per group for masked)
+    int32_t num_groups;
+    int32_t out_f32;           // 0: bf16 D, 1: f32 D
+    int32_t align_m;           // MK alignment (psum layout)
+    int32_t zero_padding;      // psum: zero-fill D rows [end, align(end))
+    int64_t lda, ldb, ldd, ldc;
+    int64_t a_gs, b_gs, d_gs, c_gs;               // group strides
+    int64_t sfa_sm, sfa_sk, sfa_gs;
+    int64_t sfb_sn, sfb_sk, sfb_gs;
+};
+
+struct TileConfig {
+    int block_m;
+    int block_n;
+};
+
+// Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
+// Throws dgm::Error on unsupported configurations or launch failures.
+void launch_fp8_gemm_1d2d(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args,
+                          hipStream_t stream);
+
+// Tile shapes compiled for the FP32-scale kernel (block_m, block_n).
+bool fp8_1d2d_tile_supported(int block_m, int block_n);
+
+// Arguments of the UE8M0 block-scaled kernel (A e4m3 or e2m1, B e4m3 or e2m1,
+// scales applied inside the scaled MFMA).
+struct Fp8Fp4GemmArgs {
+    const uint8_t* a;
+    const uint8_t* b;
+    const void* sfa;           // f32 power-of-two or packed UE8M0 int32
+    const void* sfb;
+    void* d;
+    const void* c;
+    const int32_t* layout;
+    int32_t m, n, k;           // logical K (elements)
+    int32_t num_groups;
+    int32_t out_f32;
+    int32_t align_m;
+    int32_t zero_padding;
+    int32_t a_fp4, b_fp4;
+    int32_t sfa_packed, sfb_packed;   // 1: int32 words of 4 UE8M0 bytes along K
+    int32_t gran_k_a, gran_k_b;       // 32 or 128
+    int32_t sfb_row_shift;            // SFB row = n >> shift (0, or 7 for 128-row blocks)
+    int64_t lda, ldb, ldd, ldc;       // in bytes for a/b, elements for c/d
+    int64_t a_gs, b_gs, d_gs, c_gs;   // a/b in bytes, c/d in elements
+    int64_t sfa_sm, sfa_sk, sfa_gs;   // in SF elements (floats or int32 words)
+    int64_t sfb_sn, sfb_sk, sfb_gs;
+};
+
+void launch_fp8_fp4_gemm(GemmKind kind, const TileConfig& cfg, const Fp8Fp4GemmArgs& args,
+                         hipStream_t stream);
+
+// SF layout kernels.
+struct SfTransposeArgs {
+    const float* src;
+    float* dst;
+    int32_t groups, mn, sfk;
+    int64_t s_g, s_mn, s_k;    // source strides (elements)
+    int64_t d_g, d_k;          // destination strides (d_mn == 1)
+};
+void launch_sf_transpose(const SfTransposeArgs& args, hipStream_t stream);
+
+struct SfPackArgs {
+    const float* src;
+    int32_t* dst;
+    int32_t groups, mn, sfk, packed_k;
+    int64_t s_g, s_mn, s_k;
+    int64_t d_g, d_k;          // destination strides in int32 words (d_mn == 1)
+};
+void launch_sf_pack_ue8m0(const SfPackArgs& args, hipStream_t stream);
+
+// D <- C (or zeros when c is null), used by the K == 0 early return.
+void launch_fill_or_copy(void* d, const void* c, int32_t rows, int32_t cols, int32_t groups,
+                         int64_t ldd, int64_t d_gs, int64_t ldc, int64_t c_gs, int elem_bytes,
+                         hipStream_t stream);
+
+}  // namespace dgm

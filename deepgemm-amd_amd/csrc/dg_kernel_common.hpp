@@ -1,0 +1,199 @@
+// Device-side building blocks shared by the GEMM kernels (HIP, gfx950 only).
+//
+//  * tile decode for the four row layouts (dense, m_indices-contiguous, masked,
+//    psum-contiguous) — the semantics of the reference's persistent scheduler
+//    (deep_gemm/include/deep_gemm/scheduler/gemm.cuh:146-174 get_global_idx,
+//    :185-272 get_next_block, :296-309 is_computation_valid), evaluated per
+//    workgroup;
+//  * XOR-swizzled LDS tiles of 16-byte chunks;
+//  * the predicated epilogue store of one lane's 4 consecutive outputs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "dg_internal.hpp"
+
+namespace dgm {
+namespace dev {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kE8M0One = 127;   // E8M0 encoding of 2^0
+
+__device__ __forceinline__ int align_up(int x, int a) { return (x + a - 1) / a * a; }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const __bf16 l = static_cast<__bf16>(lo);
+    const __bf16 h = static_cast<__bf16>(hi);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) << 16);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// Workgroups are handed to the 8 XCDs round-robin; give each XCD a contiguous
+// range of logical tiles so neighbouring tiles (which share A rows or B
+// columns) meet in the same L2.
+__device__ __forceinline__ int xcd_remap(int bid, int grid) {
+    if ((grid & 7) != 0) return bid;
+    return (bid & 7) * (grid >> 3) + (bid >> 3);
+}
+
+// Byte offset of 16-byte chunk `c` of row `r` in an LDS tile whose rows are
+// ROW_BYTES (128 or 64) long. The XOR keeps 8 consecutive rows at one logical
+// chunk on 8 distinct bank groups, and 8 consecutive chunk writes too.
+template <int ROW_BYTES>
+__device__ __forceinline__ int swz(int r, int c) {
+    if constexpr (ROW_BYTES == 128) {
+        return r * 128 + ((c ^ (r & 7)) << 4);
+    } else {
+        static_assert(ROW_BYTES == 64, "row pitch");
+        return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
+    }
+}
+
+// What one workgroup does for its (group, m-block, n-block).
+struct Tile {
+    int g;         // group for masked (A/D offset)
+    int expert;    // B / SFB group
+    int m0, n0;
+    int row_end;   // rows [m0, row_end) hold data
+    int pad_end;   // psum + zero padding: rows [row_end, pad_end) get zeros
+    int active;    // 0: nothing to compute (the block may still have been zero-filled)
+};
+
+// `layout` is m_indices (contiguous), masked_m (masked) or psum ends (psum).
+template <int BM, int BN, int KIND>
+__device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const int32_t* __restrict__ layout,
+                                            int align_m, int zero_padding, int num_m_blocks, int num_n_blocks,
+                                            uint16_t* zero_d, int64_t ldd, int* s_flag) {
+    Tile t{};
+    int tile = xcd_remap(blockIdx.x, gridDim.x);
+    if constexpr (KIND == kMasked) {
+        const int per_group = num_m_blocks * num_n_blocks;
+        t.g = tile / per_group;
+        tile -= t.g * per_group;
+    }
+    t.m0 = (tile % num_m_blocks) * BM;
+    t.n0 = (tile / num_m_blocks) * BN;
+    t.row_end = m;
+    t.active = 1;
+    if constexpr (KIND == kMasked) {
+        t.row_end = min(m, layout[t.g]);
+        t.expert = t.g;
+        t.active = t.m0 < t.row_end;
+    } else if constexpr (KIND == kContiguous) {
+        // Expert of the block = max(0, m_indices[first row]) (scheduler/gemm.cuh:150-153);
+        // a block whose rows are all padding does nothing.
+        // Ids past the last group are clamped so a malformed layout cannot read outside B.
+        t.expert = min(max(0, layout[t.m0]), num_groups - 1);
+        if (threadIdx.x == 0) *s_flag = 0;
+        __syncthreads();
+        if (threadIdx.x < BM && t.m0 + (int)threadIdx.x < m && layout[t.m0 + threadIdx.x] >= 0) *s_flag = 1;
+        __syncthreads();
+        t.active = *s_flag;
+    } else if constexpr (KIND == kPsum) {
+        // Group i owns rows [align(end[i-1]), end[i]); rows [end[i], align(end[i]))
+        // are padding (scheduler/gemm.cuh:205-225). block_m divides the alignment,
+        // so a block never straddles two groups.
+        int gi = 0, end = 0, aend = 0;
+        for (; gi < num_groups; ++gi) {
+            end = layout[gi];
+            aend = align_up(end, align_m);
+            if (t.m0 < aend) break;
+        }
+        if (gi == num_groups) {
+            t.active = 0;
+            return t;
+        }
+        // Rows are clipped to the m rows of A / D whatever the layout says.
+        end = min(end, m);
+        aend = min(aend, m);
+        t.expert = gi;
+        t.row_end = end;
+        t.pad_end = zero_padding ? aend : 0;
+        if (t.m0 >= end) {
+            t.active = 0;
+            if (zero_padding) {
+                const int r_hi = min(t.m0 + BM, aend);
+                for (int idx = threadIdx.x; idx < (r_hi - t.m0) * BN; idx += kThreads) {
+                    const int r = t.m0 + idx / BN, c = t.n0 + idx % BN;
+                    if (c < n) zero_d[(int64_t)r * ldd + c] = 0;
+                }
+            }
+        }
+    }
+    return t;
+}
+
+// Whether row `mrow` of this tile is stored (and whether as zeros).
+template <int KIND>
+__device__ __forceinline__ void row_predicate(const Tile& t, int m, const int32_t* __restrict__ layout, int mrow,
+                                              bool& store, bool& zero) {
+    zero = false;
+    if constexpr (KIND == kNormal) {
+        store = mrow < m;
+    } else if constexpr (KIND == kMasked) {
+        store = mrow < t.row_end;
+    } else if constexpr (KIND == kContiguous) {
+        store = mrow < m && layout[mrow] >= 0;
+    } else {
+        store = mrow < t.row_end;
+        zero = !store && mrow < t.pad_end;
+    }
+}
+
+// Store v[0..3] to D[row][n .. n+3] (D = C + v when HAS_C), clipped at n_total.
+template <int OUT_F32, int HAS_C>
+__device__ __forceinline__ void store4(void* __restrict__ d, const void* __restrict__ c, int64_t d_off,
+                                       int64_t c_off, int n, int n_total, float v0, float v1, float v2,
+                                       float v3) {
+    float v[4] = {v0, v1, v2, v3};
+    const bool full = n + 4 <= n_total;
+    if constexpr (OUT_F32) {
+        float* dp = static_cast<float*>(d) + d_off;
+        if constexpr (HAS_C) {
+            const float* cp = static_cast<const float*>(c) + c_off;
+            if (full) {
+                const f32x4 cv = *reinterpret_cast<const f32x4*>(cp);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = cv[e] + v[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < n_total) v[e] = cp[e] + v[e];
+            }
+        }
+        if (full) {
+            *reinterpret_cast<f32x4*>(dp) = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n + e < n_total) dp[e] = v[e];
+        }
+    } else {
+        uint16_t* dp = static_cast<uint16_t*>(d) + d_off;
+        if constexpr (HAS_C) {
+            const uint16_t* cp = static_cast<const uint16_t*>(c) + c_off;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n + e < n_total) v[e] = bf16_to_f32(cp[e]) + v[e];
+        }
+        if (full) {
+            *reinterpret_cast<uint2*>(dp) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n + e < n_total) dp[e] = bf16_bits(v[e]);
+        }
+    }
+}
+
+}  // namespace dev
+}  // namespace dgm

@@ -1,0 +1,312 @@
+"""deep_gemm — MI355X (gfx950) FP8 block-scaled GEMMs with DeepGEMM's Python API.
+
+Drop-in for the FP8/FP4 GEMM entry points of DeepGEMM 2.8.1
+(reference: deep_gemm/__init__.py:15-127, signatures csrc/apis/gemm.hpp:835-930,
+csrc/apis/layout.hpp:118-141, csrc/apis/config.hpp:8-47). Every GEMM runs
+hand-written HIP kernels from libdeepgemm_mi355x.so through its C ABI; there is
+no fallback path. Tensors must live on the GPU; D is written in place and the
+functions return None. Launches are asynchronous on the current stream.
+
+Scope: fp8_gemm_nt (and its fp8_fp4/fp4 aliases and nn/tn/tt transposing
+wrappers), m_grouped_fp8_gemm_nt_contiguous (m_indices and psum layouts),
+m_grouped_fp8_gemm_nt_masked, and the SF layout helpers. The reference's
+BF16/einsum/attention/Mega-MoE/cuBLASLt kernels are not provided.
+"""
+from typing import Optional, Tuple
+
+import torch
+
+from . import _ffi
+from ._ffi import check as _check, describe as _desc, ref as _ref
+
+__version__ = '2.8.1+mi355x'
+
+_lib = _ffi.lib
+_check(_lib.dg_init())
+
+
+# ------------------------------------------------------------------ config knobs
+
+def init(library_root_path: Optional[str] = None, cuda_home: Optional[str] = None) -> None:
+    """Reset the library knobs (reference `_C.init`; kernels are precompiled)."""
+    _check(_lib.dg_init())
+
+
+def shutdown() -> None:
+    _check(_lib.dg_shutdown())
+
+
+def set_num_sms(new_num_sms: int) -> None:
+    """Number of compute units the kernels may assume (MI355X: 256)."""
+    _check(_lib.dg_set_num_sms(int(new_num_sms)))
+
+
+def get_num_sms() -> int:
+    out = _ffi.ctypes.c_int32()
+    _check(_lib.dg_get_num_sms(_ffi.ctypes.byref(out)))
+    return out.value
+
+
+_py_knobs = {'tc_util': 100, 'pdl': False, 'deterministic': True, 'ignore_compile_dims': False,
+             'block_size_multiple_of': (1, 1)}
+
+
+def set_tc_util(new_tc_util: int) -> None:
+    """Accepted for compatibility; the gfx950 kernels have no tensor-core throttle."""
+    _py_knobs['tc_util'] = int(new_tc_util)
+
+
+def get_tc_util() -> int:
+    return _py_knobs['tc_util']
+
+
+def set_pdl(new_enable_pdl: bool) -> None:
+    """Accepted for compatibility; programmatic dependent launch is an NVIDIA feature."""
+    _py_knobs['pdl'] = bool(new_enable_pdl)
+
+
+def get_pdl() -> bool:
+    return _py_knobs['pdl']
+
+
+def use_deterministic_algorithms(enabled: bool) -> None:
+    """Accepted for compatibility; every kernel here is bitwise deterministic."""
+    _py_knobs['deterministic'] = bool(enabled)
+
+
+def set_ignore_compile_dims(new_value: bool) -> None:
+    """Accepted for compatibility; kernels are not specialised on M/N/K."""
+    _py_knobs['ignore_compile_dims'] = bool(new_value)
+
+
+def set_block_size_multiple_of(new_value) -> None:
+    _py_knobs['block_size_multiple_of'] = new_value if isinstance(new_value, tuple) else (new_value, new_value)
+
+
+def set_mk_alignment_for_contiguous_layout(new_value: int) -> None:
+    _check(_lib.dg_set_mk_alignment_for_contiguous_layout(int(new_value)))
+
+
+def get_mk_alignment_for_contiguous_layout() -> int:
+    return int(_lib.dg_get_mk_alignment_for_contiguous_layout())
+
+
+def get_theoretical_mk_alignment_for_contiguous_layout(expected_m: Optional[int] = None) -> int:
+    return int(_lib.dg_get_theoretical_mk_alignment_for_contiguous_layout(-1 if expected_m is None else int(expected_m)))
+
+
+# ------------------------------------------------------------------ epilogues
+
+class _EpilogueNamespace:
+    """Stand-in for the reference's `_C.epilogue` classes: only Identity is implemented."""
+
+    class Identity:
+        pass
+
+    class Alpha:
+        def __init__(self, *args, **kwargs):
+            raise RuntimeError('Unsupported error: the Alpha epilogue is not provided on gfx950')
+
+    class FP8Quantization:
+        def __init__(self, *args, **kwargs):
+            raise RuntimeError('Unsupported error: the FP8Quantization epilogue is not provided on gfx950')
+
+    class BF16StochasticRounding:
+        def __init__(self, *args, **kwargs):
+            raise RuntimeError('Unsupported error: the BF16StochasticRounding epilogue is not provided on gfx950')
+
+
+epilogue = _EpilogueNamespace()
+
+
+def _check_epilogue(ep, alpha=None):
+    if ep is not None and not isinstance(ep, _EpilogueNamespace.Identity):
+        raise RuntimeError('Assertion error (gemm.hpp): epilogue_class == nullptr and "Custom epilogues are not provided"')
+    if alpha is not None:
+        # The reference's FP32-scale (SM90) path rejects alpha the same way (csrc/apis/gemm.hpp:118).
+        raise RuntimeError('Assertion error (gemm.hpp:118): not alpha.has_value() and "FP8 GEMM alpha is not provided"')
+
+
+def _pair(x, name):
+    if not (isinstance(x, (tuple, list)) and len(x) == 2):
+        raise TypeError(f'{name} must be a (tensor, scaling factor) pair')
+    return x[0], x[1]
+
+
+# ------------------------------------------------------------------ GEMMs
+
+def fp8_fp4_gemm_nt(a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.Tensor, torch.Tensor], d: torch.Tensor,
+                    c: Optional[torch.Tensor] = None, recipe: Optional[Tuple[int, int, int]] = None,
+                    recipe_a: Optional[Tuple[int, int]] = None, recipe_b: Optional[Tuple[int, int]] = None,
+                    compiled_dims: str = 'nk', disable_ue8m0_cast: bool = False, alpha: Optional[float] = None,
+                    epilogue=None) -> None:
+    """D = C + A @ B.T with block scales (reference csrc/apis/gemm.hpp:78-133)."""
+    _check_epilogue(epilogue, alpha)
+    a_t, sfa = _pair(a, 'a')
+    b_t, sfb = _pair(b, 'b')
+    da, dsa, db, dsb, dd = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d)
+    dc = _desc(c) if c is not None else None
+    r = _ffi.recipe_struct(recipe, recipe_a, recipe_b)
+    _check(_lib.dg_fp8_fp4_gemm_nt(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dc), _ref(r),
+                                   int(bool(disable_ue8m0_cast)), _ffi.stream_of(d)))
+
+
+def fp8_fp4_gemm_nn(a, b, d, c=None, recipe=None, recipe_a=None, recipe_b=None, compiled_dims='nk',
+                    disable_ue8m0_cast=False, alpha=None, epilogue=None) -> None:
+    """Transposing wrapper (reference csrc/apis/gemm.hpp:135-148)."""
+    fp8_fp4_gemm_nt(a, (b[0].transpose(0, 1), b[1].transpose(0, 1)), d, c, recipe, recipe_a, recipe_b,
+                    compiled_dims, disable_ue8m0_cast, alpha, epilogue)
+
+
+def fp8_fp4_gemm_tn(a, b, d, c=None, recipe=None, recipe_a=None, recipe_b=None, compiled_dims='mn',
+                    disable_ue8m0_cast=False, alpha=None, epilogue=None) -> None:
+    """Transposing wrapper (reference csrc/apis/gemm.hpp:150-164)."""
+    fp8_fp4_gemm_nt((a[0].transpose(0, 1), a[1].transpose(0, 1)), (b[0].transpose(0, 1), b[1].transpose(0, 1)),
+                    d, c, recipe, recipe_a, recipe_b, compiled_dims, disable_ue8m0_cast, alpha, epilogue)
+
+
+def fp8_fp4_gemm_tt(a, b, d, c=None, recipe=None, recipe_a=None, recipe_b=None, compiled_dims='mn',
+                    disable_ue8m0_cast=False, alpha=None, epilogue=None) -> None:
+    """Transposing wrapper (reference csrc/apis/gemm.hpp:166-179)."""
+    fp8_fp4_gemm_nt((a[0].transpose(0, 1), a[1].transpose(0, 1)), b, d, c, recipe, recipe_a, recipe_b,
+                    compiled_dims, disable_ue8m0_cast, alpha, epilogue)
+
+
+def m_grouped_fp8_fp4_gemm_nt_contiguous(a, b, d: torch.Tensor, grouped_layout: torch.Tensor,
+                                         recipe=None, recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
+                                         disable_ue8m0_cast: bool = False, use_psum_layout: bool = False,
+                                         ensure_zero_padding: bool = True,
+                                         expected_m_for_psum_layout: Optional[int] = None, epilogue=None) -> None:
+    """D[r] = A[r] @ B[e(r)].T over 128-row-aligned expert segments
+    (reference csrc/apis/gemm.hpp:181-250). Rows with grouped_layout == -1 are
+    left untouched."""
+    _check_epilogue(epilogue)
+    a_t, sfa = _pair(a, 'a')
+    b_t, sfb = _pair(b, 'b')
+    da, dsa, db, dsb, dd, dl = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d), _desc(grouped_layout)
+    r = _ffi.recipe_struct(recipe, recipe_a, recipe_b)
+    _check(_lib.dg_m_grouped_fp8_fp4_gemm_nt_contiguous(
+        _ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dl), _ref(r), int(bool(disable_ue8m0_cast)),
+        int(bool(use_psum_layout)), int(bool(ensure_zero_padding)),
+        -1 if expected_m_for_psum_layout is None else int(expected_m_for_psum_layout), _ffi.stream_of(d)))
+
+
+def m_grouped_fp8_fp4_gemm_nn_contiguous(a, b, d, grouped_layout, recipe=None, recipe_a=None, recipe_b=None,
+                                         compiled_dims='nk', disable_ue8m0_cast=False, use_psum_layout=False,
+                                         ensure_zero_padding=True, epilogue=None) -> None:
+    """Transposing wrapper (reference csrc/apis/gemm.hpp:252-267)."""
+    m_grouped_fp8_fp4_gemm_nt_contiguous(a, (b[0].transpose(1, 2), b[1].transpose(1, 2)), d, grouped_layout,
+                                         recipe, recipe_a, recipe_b, compiled_dims, disable_ue8m0_cast,
+                                         use_psum_layout, ensure_zero_padding, None, epilogue)
+
+
+def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d: torch.Tensor, masked_m: torch.Tensor, expected_m: int,
+                                     recipe=None, recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
+                                     disable_ue8m0_cast: bool = False, epilogue=None) -> None:
+    """D[g, r] = A[g, r] @ B[g].T for r < masked_m[g] (reference
+    csrc/apis/gemm.hpp:269-318). Rows >= masked_m[g] are left untouched."""
+    _check_epilogue(epilogue)
+    a_t, sfa = _pair(a, 'a')
+    b_t, sfb = _pair(b, 'b')
+    da, dsa, db, dsb, dd, dm = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d), _desc(masked_m)
+    r = _ffi.recipe_struct(recipe, recipe_a, recipe_b)
+    _check(_lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(
+        _ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dm), int(expected_m), _ref(r),
+        int(bool(disable_ue8m0_cast)), _ffi.stream_of(d)))
+
+
+# Aliases (reference csrc/apis/gemm.hpp:920-930)
+fp4_gemm_nt = fp8_fp4_gemm_nt
+fp8_gemm_nt = fp8_fp4_gemm_nt
+fp8_gemm_nn = fp8_fp4_gemm_nn
+fp8_gemm_tn = fp8_fp4_gemm_tn
+fp8_gemm_tt = fp8_fp4_gemm_tt
+m_grouped_fp4_gemm_nt_contiguous = m_grouped_fp8_fp4_gemm_nt_contiguous
+m_grouped_fp8_gemm_nt_contiguous = m_grouped_fp8_fp4_gemm_nt_contiguous
+m_grouped_fp8_gemm_nn_contiguous = m_grouped_fp8_fp4_gemm_nn_contiguous
+m_grouped_fp4_gemm_nt_masked = m_grouped_fp8_fp4_gemm_nt_masked
+m_grouped_fp8_gemm_nt_masked = m_grouped_fp8_fp4_gemm_nt_masked
+
+
+# ------------------------------------------------------------------ SF layouts
+
+def get_tma_aligned_size(x: int, element_size: int) -> int:
+    out = _ffi.ctypes.c_int32()
+    _check(_lib.dg_get_tma_aligned_size(int(x), int(element_size), _ffi.ctypes.byref(out)))
+    return out.value
+
+
+def get_mn_major_tma_aligned_tensor(sf: torch.Tensor) -> torch.Tensor:
+    """FP32 SF -> MN-major copy with row pitch align(mn, 4)
+    (reference csrc/jit_kernels/impls/smxx_layout.hpp:60-106)."""
+    if sf.dim() not in (2, 3) or sf.dtype != torch.float:
+        raise RuntimeError('Assertion error (smxx_layout.hpp:50-51): dim == 2 or dim == 3; sf.scalar_type() == torch::kFloat')
+    batched = sf.unsqueeze(0) if sf.dim() == 2 else sf
+    g, mn, sfk = batched.shape
+    amn = get_tma_aligned_size(mn, 4)
+    if (batched.stride(0) == amn * sfk or sf.dim() == 2) and batched.stride(1) == 1 and batched.stride(2) == amn:
+        return sf
+    out = torch.empty_strided((g, mn, sfk), (amn * sfk, 1, amn), dtype=torch.float, device=sf.device)
+    _check(_lib.dg_get_mn_major_tma_aligned_tensor(_ref(_desc(batched)), _ref(_desc(out)), _ffi.stream_of(out)))
+    return out.squeeze(0) if sf.dim() == 2 else out
+
+
+def get_mn_major_tma_aligned_packed_ue8m0_tensor(sf: torch.Tensor, psum_layout: Optional[torch.Tensor] = None):
+    """FP32 power-of-two SF -> MN-major int32 words of 4 UE8M0 bytes along K
+    (reference csrc/jit_kernels/impls/smxx_layout.hpp:133-216). `psum_layout`
+    is accepted for compatibility; gap rows are packed like any other row."""
+    if sf.dim() not in (2, 3) or sf.dtype != torch.float:
+        raise RuntimeError('Assertion error (smxx_layout.hpp:50-51): dim == 2 or dim == 3; sf.scalar_type() == torch::kFloat')
+    batched = sf.unsqueeze(0) if sf.dim() == 2 else sf
+    g, mn, sfk = batched.shape
+    amn = get_tma_aligned_size(mn, 4)
+    pk = (sfk + 3) // 4
+    out = torch.empty_strided((g, mn, pk), (amn * pk, 1, amn), dtype=torch.int32, device=sf.device)
+    _check(_lib.dg_get_mn_major_tma_aligned_packed_ue8m0_tensor(_ref(_desc(batched)), _ref(_desc(out)),
+                                                                _ffi.stream_of(out)))
+    return out.squeeze(0) if sf.dim() == 2 else out
+
+
+def transform_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe, num_groups: Optional[int] = None,
+                                      is_sfa: Optional[bool] = None, disable_ue8m0_cast: bool = False,
+                                      psum_layout: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Reference csrc/apis/layout.hpp:11-58 for this device."""
+    recipe = tuple(int(v) for v in recipe)
+    r3 = r2 = None
+    if len(recipe) == 3:
+        r3 = (_ffi.ctypes.c_int32 * 3)(*recipe)
+    elif len(recipe) == 2:
+        r2 = (_ffi.ctypes.c_int32 * 2)(*recipe)
+    else:
+        raise RuntimeError('Assertion error (layout.hpp:31): Invalid recipe')
+    kind = _ffi.ctypes.c_int32()
+    _check(_lib.dg_plan_sf_transform(_ref(_desc(sf)), int(mn), int(k), r3, r2,
+                                     -1 if num_groups is None else int(num_groups),
+                                     -1 if is_sfa is None else int(bool(is_sfa)), int(bool(disable_ue8m0_cast)),
+                                     _ffi.ctypes.byref(kind)))
+    if kind.value == 0:
+        return sf
+    if kind.value == 1:
+        return get_mn_major_tma_aligned_tensor(sf)
+    gran_mn = recipe[0] if len(recipe) == 2 else (recipe[0] if is_sfa else recipe[1])
+    if gran_mn != 1:
+        rows = torch.arange(mn, device=sf.device) // gran_mn
+        sf = sf.index_select(-2, rows)
+    return get_mn_major_tma_aligned_packed_ue8m0_tensor(sf, psum_layout)
+
+
+# ------------------------------------------------------------------ introspection
+
+def set_tile_override(block_m: int = 0, block_n: int = 0) -> None:
+    """Force the FP32-scale kernel's tile (0, 0 = heuristic). Testing/tuning aid."""
+    _check(_lib.dg_set_tile_override(int(block_m), int(block_n)))
+
+
+def get_last_config() -> str:
+    """Kernel configuration chosen by the last GEMM call on this thread."""
+    return _ffi.last_config()
+
+
+from . import testing  # noqa: E402
+from . import utils  # noqa: E402
+from .utils import *  # noqa: E402,F401,F403

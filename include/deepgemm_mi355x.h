@@ -1,0 +1,211 @@
+/*
+ * deepgemm_mi355x.h — C ABI of the MI355X (gfx950) FP8 block-scaled GEMM library.
+ *
+ * Drop-in for the FP8 GEMM entry points of DeepGEMM's pybind module `deep_gemm._C`
+ * (reference: csrc/apis/gemm.hpp, csrc/apis/layout.hpp, csrc/apis/config.hpp,
+ * registered in csrc/python_api.cpp:24-49). Every entry point:
+ *   - takes plain pointers and sizes (no framework types);
+ *   - validates everything on the host before touching the GPU, with the
+ *     reference's checks (csrc/utils/layout.hpp:19-140, csrc/apis/gemm.hpp:17-318);
+ *   - launches asynchronously on the given HIP stream (hipStream_t passed as
+ *     void*, NULL = the null stream) and never synchronizes;
+ *   - never throws; returns DG_OK or an error code, with the message available
+ *     from dg_last_error() (thread-local), formatted like the reference's
+ *     DGException: "Assertion error (file:line): condition"
+ *     (csrc/utils/exception.hpp:13-37);
+ *   - never retains a pointer after it returns. The caller owns all memory,
+ *     including outputs, which are written in place.
+ */
+#ifndef DEEPGEMM_MI355X_H
+#define DEEPGEMM_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DG_ABI_VERSION 1
+
+/* Return codes. */
+enum dg_status {
+    DG_OK = 0,
+    DG_ERR_INVALID = 1,      /* an argument check failed (reference: DG_HOST_ASSERT) */
+    DG_ERR_UNSUPPORTED = 2,  /* valid for the reference but not provided here */
+    DG_ERR_HIP = 3,          /* a HIP runtime call failed */
+    DG_ERR_INTERNAL = 4
+};
+
+/* Element types. DG_I8 holds packed FP4 E2M1 pairs (reference kPackedFP4 = torch.int8,
+ * csrc/utils/math.hpp:11): element 2i in the low nibble. */
+enum dg_dtype {
+    DG_F32 = 0,
+    DG_BF16 = 1,
+    DG_E4M3 = 2,   /* OCP float8_e4m3fn */
+    DG_I32 = 3,
+    DG_I8 = 4,
+    DG_U8 = 5,
+    DG_F16 = 6,
+    DG_I64 = 7
+};
+
+/* A strided tensor view. Strides are in elements; device is the HIP device
+ * ordinal, or -1 for host memory (rejected by every compute entry point, as the
+ * reference's get_shape asserts is_cuda, csrc/utils/layout.hpp:48-55). */
+typedef struct dg_tensor {
+    void*   data;
+    int32_t dtype;
+    int32_t ndim;
+    int64_t sizes[4];
+    int64_t strides[4];
+    int32_t device;
+    int32_t reserved;
+} dg_tensor;
+
+/* Scaling-factor recipe. Either `recipe` (gran_m, gran_n, gran_k) or the pair
+ * `recipe_a` / `recipe_b` (gran_mn, gran_k), never both (csrc/apis/layout.hpp:71-77).
+ * Passing NULL, or has_recipe == has_recipe_ab == 0, selects the default recipe
+ * (1, 128, 128) for FP32 scales (csrc/utils/layout.hpp:86-98). */
+typedef struct dg_recipe {
+    int32_t has_recipe;
+    int32_t recipe[3];
+    int32_t has_recipe_ab;
+    int32_t recipe_a[2];
+    int32_t recipe_b[2];
+} dg_recipe;
+
+/* ---------------------------------------------------------------- lifecycle */
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* dg_last_error(void);
+
+/* Library version string. */
+const char* dg_version(void);
+
+/* Replaces `_C.init(library_root_path, cuda_home)` (deep_gemm/__init__.py:122,
+ * csrc/apis/config.hpp:9-11). Kernels are precompiled, so there is nothing to
+ * JIT; the call only resets the knobs below to their defaults. No device work. */
+int dg_init(void);
+
+/* Replaces `_C.shutdown` (deep_gemm/__init__.py:125, csrc/apis/config.hpp:12-14). */
+int dg_shutdown(void);
+
+/* ---------------------------------------------------------------- GEMMs */
+
+/* D = C + A @ B^T with block scales.
+ * Replaces fp8_fp4_gemm_nt / fp8_gemm_nt / fp4_gemm_nt (csrc/apis/gemm.hpp:78-133,
+ * registered :838-845, aliases :921-922).
+ *   a    [M, K] e4m3 (or [M, K/2] packed e2m1), K-major
+ *   sfa  FP32 [M, ceil(K/gran_k_a)] (any strides) or packed UE8M0 int32
+ *   b    [N, K] e4m3 (or [N, K/2] packed e2m1), K-major
+ *   sfb  FP32 [ceil(N/gran_n), ceil(K/gran_k_b)] or packed UE8M0 int32
+ *   d    [M, N] bf16 or fp32, row-major
+ *   c    NULL, or [M, N] with d's dtype (may alias d: in-place accumulate)
+ * disable_ue8m0_cast: reference flag (csrc/apis/gemm.hpp:88); FP32 SFs of the
+ * (1,128,128) recipe always take the FP32-scale path. */
+int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa,
+                       const dg_tensor* b, const dg_tensor* sfb,
+                       const dg_tensor* d, const dg_tensor* c,
+                       const dg_recipe* recipe,
+                       int32_t disable_ue8m0_cast,
+                       void* stream);
+
+/* M-grouped contiguous GEMM (prefill MoE).
+ * Replaces m_grouped_fp8_fp4_gemm_nt_contiguous / m_grouped_fp8_gemm_nt_contiguous
+ * (csrc/apis/gemm.hpp:181-250, registered :870-879, aliases :926-927).
+ *   a [M, K], b [G, N, K], d [M, N] bf16, grouped_layout int32 [M] on the device:
+ *   the expert of rows [i*align, (i+1)*align) is max(0, grouped_layout[i*align])
+ *   and rows with grouped_layout < 0 are padding, left untouched.
+ * use_psum_layout / ensure_zero_padding / expected_m_for_psum_layout (< 0 = None)
+ * are the reference's arguments (psum layout: grouped_layout int32 [G] of
+ * cumulative end offsets, each group starting at the previous end aligned up to
+ * the MK alignment). */
+int dg_m_grouped_fp8_fp4_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor* sfa,
+                                            const dg_tensor* b, const dg_tensor* sfb,
+                                            const dg_tensor* d,
+                                            const dg_tensor* grouped_layout,
+                                            const dg_recipe* recipe,
+                                            int32_t disable_ue8m0_cast,
+                                            int32_t use_psum_layout,
+                                            int32_t ensure_zero_padding,
+                                            int32_t expected_m_for_psum_layout,
+                                            void* stream);
+
+/* M-grouped masked GEMM (decode MoE).
+ * Replaces m_grouped_fp8_fp4_gemm_nt_masked / m_grouped_fp8_gemm_nt_masked
+ * (csrc/apis/gemm.hpp:269-318, registered :889-894, aliases :929-930).
+ *   a [G, max_m, K], b [G, N, K], d [G, max_m, N] bf16, masked_m int32 [G] on the
+ *   device. Rows r >= masked_m[g] of group g are left untouched. expected_m only
+ *   steers the tile choice (csrc/jit_kernels/impls/sm90_fp8_gemm_1d2d.hpp:238). */
+int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa,
+                                        const dg_tensor* b, const dg_tensor* sfb,
+                                        const dg_tensor* d,
+                                        const dg_tensor* masked_m,
+                                        int32_t expected_m,
+                                        const dg_recipe* recipe,
+                                        int32_t disable_ue8m0_cast,
+                                        void* stream);
+
+/* ---------------------------------------------------------------- SF layouts */
+
+/* Replaces get_tma_aligned_size (csrc/utils/math.hpp:23-27, registered
+ * csrc/apis/layout.hpp:126): x aligned up to 16 bytes worth of elements. */
+int dg_get_tma_aligned_size(int32_t x, int32_t element_size, int32_t* out);
+
+/* Replaces get_mn_major_tma_aligned_tensor (csrc/jit_kernels/impls/smxx_layout.hpp:60-106,
+ * registered csrc/apis/layout.hpp:127). Copies FP32 `sf` ([mn, sf_k] or
+ * [G, mn, sf_k], any strides) into `out`, which the caller allocates with sizes
+ * equal to sf's and strides (align(mn,4)*sf_k, 1, align(mn,4)). Bit-exact copy. */
+int dg_get_mn_major_tma_aligned_tensor(const dg_tensor* sf, const dg_tensor* out, void* stream);
+
+/* Replaces get_mn_major_tma_aligned_packed_ue8m0_tensor
+ * (csrc/jit_kernels/impls/smxx_layout.hpp:133-216, registered csrc/apis/layout.hpp:128).
+ * FP32 power-of-two `sf` [.., mn, k] -> int32 `out` [.., mn, ceil(k/4)] with
+ * strides (align(mn,4)*ceil(k/4), 1, align(mn,4)); byte j of a word is the
+ * exponent of K index 4*word+j, padding bytes zero. */
+int dg_get_mn_major_tma_aligned_packed_ue8m0_tensor(const dg_tensor* sf, const dg_tensor* out,
+                                                    void* stream);
+
+/* Planning half of transform_sf_into_required_layout (csrc/apis/layout.hpp:11-58):
+ * runs the reference's checks for `sf` and reports what the transform does.
+ * *kind = 0: use sf as is; 1: MN-major TMA-aligned FP32 copy
+ * (dg_get_mn_major_tma_aligned_tensor); 2: packed UE8M0
+ * (dg_get_mn_major_tma_aligned_packed_ue8m0_tensor), after broadcasting rows by
+ * gran_mn when gran_mn > 1. recipe3 (3 ints) with is_sfa (0/1), or recipe2 (2
+ * ints) with is_sfa = -1; num_groups < 0 = None. */
+int dg_plan_sf_transform(const dg_tensor* sf, int32_t mn, int32_t k,
+                         const int32_t* recipe3, const int32_t* recipe2,
+                         int32_t num_groups, int32_t is_sfa,
+                         int32_t disable_ue8m0_cast, int32_t* kind);
+
+/* ---------------------------------------------------------------- knobs */
+
+/* Replace set_num_sms / get_num_sms (csrc/apis/config.hpp:15-20,
+ * csrc/runtime/runtime.hpp:78-87). On MI355X these count compute units (256).
+ * The getter reads the current device's CU count on first use. */
+int dg_set_num_sms(int32_t num_sms);
+int dg_get_num_sms(int32_t* out);
+
+/* Replace set/get_mk_alignment_for_contiguous_layout and
+ * get_theoretical_mk_alignment_for_contiguous_layout
+ * (csrc/jit_kernels/heuristics/runtime.hpp:49-63, registered csrc/apis/layout.hpp:133-141).
+ * Default 128. expected_m < 0 = None. */
+int dg_set_mk_alignment_for_contiguous_layout(int32_t alignment);
+int32_t dg_get_mk_alignment_for_contiguous_layout(void);
+int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m);
+
+/* Tile override for tests and tuning (no reference counterpart; the reference's
+ * closest knob is DG_JIT_* config printing). block_m = block_n = 0 restores the
+ * heuristic. Only listed tile shapes are accepted. */
+int dg_set_tile_override(int32_t block_m, int32_t block_n);
+
+/* Describes the kernel configuration the last GEMM call on this thread chose
+ * (reference: DG_PRINT_CONFIGS, csrc/jit_kernels/heuristics/common.hpp:44-54).
+ * Writes a NUL-terminated string of at most `cap` bytes. */
+int dg_last_config(char* buf, int32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DEEPGEMM_MI355X_H */

@@ -1,0 +1,151 @@
+"""Reference GEMMs, grouping rules, SF layout transforms and metrics (numpy).
+
+TEST INFRASTRUCTURE: see ``oracle/__init__.py``.
+
+All GEMM references dequantize in float32 exactly as the caller would
+(``deep_gemm/utils/math.py:170-176`` ``cast_back_from_fp8``: fp8 value x SF as a
+float32 product) and then multiply in float64, so the only rounding left on the
+reference side is the final float64 -> output cast done by the test.
+
+Functions and what they follow:
+
+* ``calc_diff``            -- ``deep_gemm/testing/numeric.py:5-11``.
+* ``gemm_nt``              -- D = C + A.B^T on dequantized operands
+                              (``csrc/apis/gemm.hpp:78-133``; C semantics of
+                              ``early_return`` ``:17-53``).
+* ``contiguous_expert_of_block`` / ``gemm_contiguous``
+                           -- expert of an M-block is ``max(0, layout[block*BM])``
+                              (``scheduler/gemm.cuh:150-153``); rows with layout
+                              < 0 are padding (``:299-300``) and stay untouched.
+* ``gemm_masked``          -- rows r < masked_m[g] of group g are computed
+                              (``scheduler/gemm.cuh:188-204,301-302``); the rest
+                              stay untouched.
+* ``mn_major_tma_aligned`` -- ``csrc/jit_kernels/impls/smxx_layout.hpp:60-106``:
+                              values unchanged, strides (align(mn,4)*sf_k, 1, align(mn,4)).
+* ``pack_ue8m0_mn_major``  -- ``tests/test_layout.py:20-42``: exponent bytes, four
+                              per int32 along K (little end = lowest K), MN-major.
+
+Pinned by ``tests/test_oracle.py``: pure-Python triple loops on tiny shapes,
+all-ones / single-K-block closed forms, linearity in C, the grouped rules by
+brute-force enumeration, and calc_diff closed forms.
+"""
+import numpy as np
+
+from . import fp8, quant
+
+
+def calc_diff(x, y) -> float:
+    x = np.asarray(x, dtype=np.float64)
+    y = np.asarray(y, dtype=np.float64)
+    den = float((x * x + y * y).sum())
+    if den == 0.0:
+        return 0.0
+    return 1.0 - 2.0 * float((x * y).sum()) / den
+
+
+def max_rel_err(x, ref, floor: float = 1e-2) -> float:
+    """max |x - ref| / max(|ref|, floor * rms(ref)) — scale-aware relative error."""
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if ref.size == 0:
+        return 0.0
+    rms = float(np.sqrt((ref * ref).mean())) or 1.0
+    den = np.maximum(np.abs(ref), floor * rms)
+    return float((np.abs(x - ref) / den).max())
+
+
+def gemm_nt(a_deq: np.ndarray, b_deq: np.ndarray, c: np.ndarray = None) -> np.ndarray:
+    """float64 D = C + A.B^T for A [M, K], B [N, K] (float32 dequantized)."""
+    d = a_deq.astype(np.float64) @ b_deq.astype(np.float64).T
+    if c is not None:
+        d = d + np.asarray(c, dtype=np.float64)
+    return d
+
+
+def gemm_nt_f32(a_deq: np.ndarray, b_deq: np.ndarray) -> np.ndarray:
+    """float32 D = A.B^T: the reference tests' FP32 dequantize-then-matmul, used as the
+    timed CPU baseline (the float64 `gemm_nt` is the accuracy oracle)."""
+    return np.asarray(a_deq, dtype=np.float32) @ np.asarray(b_deq, dtype=np.float32).T
+
+
+def contiguous_expert_of_block(m_indices: np.ndarray, block_m: int) -> np.ndarray:
+    """Expert id per M-block: max(0, m_indices[block * block_m])."""
+    m = m_indices.shape[0]
+    starts = np.arange(0, m, block_m)
+    return np.maximum(m_indices[starts], 0)
+
+
+def gemm_contiguous(a_deq: np.ndarray, b_deq: np.ndarray, m_indices: np.ndarray,
+                    block_m: int = 128):
+    """-> (D float64 [M, N] with NaN in padding rows, valid mask [M])."""
+    m = a_deq.shape[0]
+    n = b_deq.shape[1]
+    d = np.full((m, n), np.nan, dtype=np.float64)
+    experts = contiguous_expert_of_block(m_indices, block_m)
+    valid = m_indices >= 0
+    for blk, e in enumerate(experts):
+        r0, r1 = blk * block_m, min(m, (blk + 1) * block_m)
+        rows = np.arange(r0, r1)[valid[r0:r1]]
+        if rows.size:
+            d[rows] = a_deq[rows].astype(np.float64) @ b_deq[e].astype(np.float64).T
+    return d, valid
+
+
+def gemm_masked(a_deq: np.ndarray, b_deq: np.ndarray, masked_m: np.ndarray):
+    """A [G, max_m, K], B [G, N, K] -> (D [G, max_m, N] NaN outside, valid [G, max_m])."""
+    g, max_m, _ = a_deq.shape
+    n = b_deq.shape[1]
+    d = np.full((g, max_m, n), np.nan, dtype=np.float64)
+    valid = np.arange(max_m)[None, :] < np.asarray(masked_m)[:, None]
+    for i in range(g):
+        r = int(masked_m[i])
+        if r > 0:
+            d[i, :r] = a_deq[i, :r].astype(np.float64) @ b_deq[i].astype(np.float64).T
+    return d, valid
+
+
+def tma_aligned_size(x: int, element_size: int) -> int:
+    """``csrc/utils/math.hpp:23-27``: align x to 16 bytes worth of elements."""
+    assert 16 % element_size == 0
+    n = 16 // element_size
+    return (x + n - 1) // n * n
+
+
+def mn_major_tma_aligned(sf: np.ndarray):
+    """Return (storage [G, sf_k, align(mn,4)] float32, view [G, mn, sf_k], strides).
+
+    ``strides`` are in elements, (align(mn,4)*sf_k, 1, align(mn,4)); the view's
+    values equal the input's.
+    """
+    s3 = sf[None] if sf.ndim == 2 else sf
+    g, mn, sfk = s3.shape
+    amn = tma_aligned_size(mn, 4)
+    storage = np.zeros((g, sfk, amn), dtype=np.float32)
+    storage[:, :, :mn] = np.swapaxes(s3, 1, 2)
+    view = np.swapaxes(storage[:, :, :mn], 1, 2)
+    return storage, view, (amn * sfk, 1, amn)
+
+
+def pack_ue8m0_mn_major(sf: np.ndarray) -> np.ndarray:
+    """Power-of-two float32 SF [.., mn, k] -> int32 storage [G, align(k,4)/4, align(mn,4)].
+
+    Element (g, kk, r) packs the exponent bytes of sf[g, r, 4kk .. 4kk+3] with the
+    lowest K in the least significant byte; padding bytes are zero.
+    """
+    s3 = sf[None] if sf.ndim == 2 else sf
+    g, mn, k = s3.shape
+    amn = tma_aligned_size(mn, 4)
+    ak = (k + 3) // 4 * 4
+    e = np.zeros((g, amn, ak), dtype=np.uint8)
+    e[:, :mn, :k] = fp8.ue8m0_from_pow2_f32(s3)
+    packed = e.reshape(g, amn, ak // 4, 4).astype(np.uint32)
+    words = packed[..., 0] | (packed[..., 1] << 8) | (packed[..., 2] << 16) | (packed[..., 3] << 24)
+    return np.ascontiguousarray(np.swapaxes(words.view(np.int32), 1, 2))
+
+
+def fp8_fp4_gemm_nt(a_codes, sfa, b_packed, sfb, gran_k_a: int = 128, gran_k_b: int = 32,
+                    c=None) -> np.ndarray:
+    """A e4m3 [M, K] (1 x gran_k_a SF), B e2m1 packed [N, K/2] (1 x gran_k_b SF)."""
+    a_deq = quant.dequant_per_token(a_codes, sfa, gran_k_a)
+    b_deq = quant.dequant_fp4(b_packed, sfb, gran_k_b)
+    return gemm_nt(a_deq, b_deq, c)

@@ -1,0 +1,356 @@
+"""GPU parity of the HIP kernels against the CPU oracle (run on an MI355X).
+
+Bars (tolerances are the reference's, tests/generators.py:69-74):
+  * calc_diff(D, oracle) < 1e-3 for FP8 x FP8 (measured ~1e-6: BF16 output rounding
+    only), and the max relative error is printed; FP8 x FP4 < 1e-2.
+  * 20 reruns bitwise identical (reference tests/test_fp8_fp4.py:72-82).
+  * rows that must not be written (padding rows, rows >= masked_m, past M/N)
+    keep a sentinel byte pattern bit-exactly.
+  * a grouped call's segment equals the dense call on that segment bitwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+import deep_gemm
+from oracle import gemm as ogemm
+from oracle import quant as oquant
+import generators as gen
+
+pytestmark = pytest.mark.gpu
+
+DEV = 'cuda'
+SENTINEL = 0x7F7B   # bf16 bit pattern written before each call (a large finite value)
+
+
+def e4m3(x):
+    return gen.to_dev(x, torch.float8_e4m3fn)
+
+
+def f32(x):
+    return gen.to_dev(np.asarray(x, dtype=np.float32))
+
+
+def sentinel_bf16(shape):
+    return torch.full(shape, SENTINEL, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+
+
+def report(name, d, ref):
+    diff = ogemm.calc_diff(d, ref)
+    rel = ogemm.max_rel_err(d, ref)
+    print(f'[{name}] calc_diff={diff:.3e} max_rel_err={rel:.3e}', flush=True)
+    return diff, rel
+
+
+# ----------------------------------------------------------------- dense
+
+DENSE_CASES = [
+    (64, 2112, 7168),    # config 1 shape
+    (1, 256, 128),
+    (128, 576, 7168),
+    (129, 200, 384),     # ragged M and N, N not a multiple of 64
+    (300, 4096, 512),
+    (7, 16, 16),         # K shorter than one block
+    (256, 512, 1040),    # K tail (K % 128 == 16)
+]
+
+
+@pytest.mark.parametrize('m,n,k', DENSE_CASES)
+def test_dense_bf16_vs_oracle(m, n, k):
+    print(f'dense m={m} n={n} k={k}', flush=True)
+    x = gen.dense_inputs(m, n, k, seed=m + n + k)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    deep_gemm.fp8_gemm_nt((e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb'])), d)
+    torch.cuda.synchronize()
+    out = d.float().cpu().numpy()
+    diff, rel = report(f'dense {m}x{n}x{k}', out, ref)
+    assert diff < 1e-3
+    # Stronger than the reference bar: within one BF16 ulp of the FP64 oracle, plus the FP32
+    # accumulation error that dominates near zero (K products of magnitude <= max|ref|).
+    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref).max()
+    assert np.all(np.abs(out - ref) <= tol), 'further than one BF16 ulp from the FP64 oracle'
+    # Against the unquantized product, the reference tests' own oracle (tests/generators.py:363)
+    raw = x['a'].astype(np.float64) @ x['b'].astype(np.float64).T
+    print(f'  calc_diff vs unquantized = {ogemm.calc_diff(out, raw):.3e}', flush=True)
+    if k >= 128:
+        assert ogemm.calc_diff(out, raw) < 1e-3
+
+
+def test_all_tiles_bitwise_equal():
+    """Every compiled tile shape gives the same bits (each output's K order is fixed)."""
+    m, n, k = 200, 320, 1024
+    x = gen.dense_inputs(m, n, k, seed=5)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    outs = []
+    try:
+        for bm, bn in ((64, 64), (64, 128), (128, 64), (128, 128)):
+            deep_gemm.set_tile_override(bm, bn)
+            d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+            deep_gemm.fp8_gemm_nt(a, b, d)
+            outs.append(d)
+            print(deep_gemm.get_last_config(), flush=True)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+
+@pytest.mark.parametrize('inplace', [True, False])
+def test_dense_c_accumulate_f32(inplace):
+    m, n, k = 256, 384, 896
+    print(f'dense f32 C accumulate inplace={inplace}', flush=True)
+    x = gen.dense_inputs(m, n, k, seed=11)
+    c_np = gen.randn_bf16((m, n), 99) * 32.0
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']),
+                        c_np)
+    c = f32(c_np)
+    d = c if inplace else torch.empty((m, n), dtype=torch.float32, device=DEV)
+    deep_gemm.fp8_gemm_nt((e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb'])), d, c=c)
+    torch.cuda.synchronize()
+    out = d.cpu().numpy()
+    diff, rel = report('c-accumulate', out, ref)
+    assert diff < 1e-6
+    # D = C + (A.B^T) with one FP32 add: matches C + FP32(acc) up to the accumulation error.
+    assert np.max(np.abs(out - ref)) < 1e-3 * np.max(np.abs(ref))
+
+
+def test_dense_bf16_c_accumulate():
+    m, n, k = 128, 256, 512
+    x = gen.dense_inputs(m, n, k, seed=12)
+    c_np = oquant.bf16_round(gen.randn_bf16((m, n), 98))
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']),
+                        c_np)
+    d = gen.to_dev(c_np).bfloat16()
+    deep_gemm.fp8_gemm_nt((e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb'])), d, c=d)
+    diff, _ = report('bf16 c-accumulate', d.float().cpu().numpy(), ref)
+    assert diff < 1e-3
+
+
+def test_dense_determinism_and_bounds():
+    """20 reruns are bitwise equal; a view into a sentinel-filled buffer is written only inside the view."""
+    m, n, k = 200, 264, 2048
+    x = gen.dense_inputs(m, n, k, seed=3)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    big = sentinel_bf16((m + 8, n + 64))
+    d = big[4:4 + m, 8:8 + n]
+    deep_gemm.fp8_gemm_nt(a, b, d)
+    first = d.clone()
+    for _ in range(20):
+        d.fill_(0)
+        deep_gemm.fp8_gemm_nt(a, b, d)
+        assert torch.equal(d.view(torch.int16), first.view(torch.int16))
+    mask = torch.ones_like(big, dtype=torch.bool)
+    mask[4:4 + m, 8:8 + n] = False
+    assert bool((big.view(torch.int16)[mask] == SENTINEL).all())
+
+
+def test_mn_major_sfa_equals_k_major():
+    """SFA in the reference's MN-major TMA-aligned layout gives the same bits as K-major SFA."""
+    m, n, k = 130, 256, 1024
+    x = gen.dense_inputs(m, n, k, seed=4)
+    a_t, b = e4m3(x['qa']), (e4m3(x['qb']), f32(x['sfb']))
+    sfa = f32(x['sfa'])
+    sfa_mn = deep_gemm.get_mn_major_tma_aligned_tensor(sfa)
+    assert sfa_mn.stride() == (1, deep_gemm.get_tma_aligned_size(m, 4))
+    d1 = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    d2 = torch.empty_like(d1)
+    deep_gemm.fp8_gemm_nt((a_t, sfa), b, d1)
+    deep_gemm.fp8_gemm_nt((a_t, sfa_mn), b, d2)
+    assert torch.equal(d1.view(torch.int16), d2.view(torch.int16))
+
+
+def test_k_zero_and_empty():
+    m, n = 64, 128
+    a = torch.empty((m, 0), dtype=torch.float8_e4m3fn, device=DEV)
+    b = torch.empty((n, 0), dtype=torch.float8_e4m3fn, device=DEV)
+    sfa = torch.empty((m, 0), dtype=torch.float32, device=DEV)
+    sfb = torch.empty((1, 0), dtype=torch.float32, device=DEV)
+    d = torch.full((m, n), 3.0, dtype=torch.float32, device=DEV)
+    deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d)          # K == 0, no C -> zeros
+    assert bool((d == 0).all())
+    c = torch.randn((m, n), device=DEV)
+    deep_gemm.fp8_gemm_nt((a, sfa), (b, sfb), d, c=c)     # K == 0 with C -> D = C
+    assert torch.equal(d, c)
+    a0 = torch.empty((0, 256), dtype=torch.float8_e4m3fn, device=DEV)
+    deep_gemm.fp8_gemm_nt((a0, torch.empty((0, 2), device=DEV)),
+                          (torch.empty((n, 256), dtype=torch.float8_e4m3fn, device=DEV),
+                           torch.ones((1, 2), device=DEV)), torch.empty((0, n), dtype=torch.bfloat16, device=DEV))
+
+
+# ----------------------------------------------------------------- grouped
+
+def test_contiguous_vs_oracle_and_dense():
+    ms, aligned = gen.contiguous_sizes(4, 900, seed=7)
+    n, k = 384, 1024
+    print(f'contiguous ms={ms} aligned={aligned}', flush=True)
+    x = gen.contiguous_inputs(ms, aligned, n, k, seed=7)
+    a_deq = oquant.dequant_per_token(x['qa'], x['sfa'])
+    b_deq = np.stack([oquant.dequant_per_block(x['qb'][i], x['sfb'][i]) for i in range(len(ms))])
+    ref, valid = ogemm.gemm_contiguous(a_deq, b_deq, x['m_indices'])
+    m_pad = sum(aligned)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    mi = gen.to_dev(x['m_indices'])
+    d = sentinel_bf16((m_pad, n))
+    deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, mi)
+    torch.cuda.synchronize()
+    out = d.float().cpu().numpy()
+    report('contiguous', out[valid], ref[valid])
+    assert ogemm.calc_diff(out[valid], ref[valid]) < 1e-3
+    # padding rows untouched, bit-exact
+    assert bool((d.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
+    # each segment equals the dense call on that segment's rows (same tile shape)
+    start = 0
+    for i, (mi_, ai) in enumerate(zip(ms, aligned)):
+        if mi_ > 0:
+            dd = torch.empty((mi_, n), dtype=torch.bfloat16, device=DEV)
+            deep_gemm.fp8_gemm_nt((a[0][start:start + mi_], a[1][start:start + mi_]), (b[0][i], b[1][i]), dd)
+            assert torch.equal(dd.view(torch.int16), d[start:start + mi_].view(torch.int16)), f'segment {i}'
+        start += ai
+    # determinism
+    first = d.clone()
+    for _ in range(20):
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, mi)
+    assert torch.equal(d.view(torch.int16), first.view(torch.int16))
+
+
+def test_psum_layout():
+    g, n, k = 4, 256, 512
+    ms = [100, 0, 257, 64]
+    align = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    ends, starts, prev = [], [], 0
+    for mi in ms:
+        s = (prev + align - 1) // align * align
+        starts.append(s)
+        ends.append(s + mi)
+        prev = s + mi
+    m_pad = (ends[-1] + align - 1) // align * align
+    x = gen.contiguous_inputs(ms, [((mi + align - 1) // align) * align for mi in ms], n, k, seed=21)
+    # x rows are laid out with per-group aligned starts, identical to the psum starts above
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    psum = torch.tensor(ends, dtype=torch.int32, device=DEV)
+    for zero_pad in (False, True):
+        d = sentinel_bf16((m_pad, n))
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, psum, use_psum_layout=True,
+                                                   ensure_zero_padding=zero_pad)
+        torch.cuda.synchronize()
+        for i in range(g):
+            s, e = starts[i], ends[i]
+            if e > s:
+                dd = torch.empty((e - s, n), dtype=torch.bfloat16, device=DEV)
+                deep_gemm.fp8_gemm_nt((a[0][s:e], a[1][s:e]), (b[0][i], b[1][i]), dd)
+                assert torch.equal(dd.view(torch.int16), d[s:e].view(torch.int16)), f'group {i}'
+            pe = (e + align - 1) // align * align
+            pad = d[e:pe].view(torch.int16)
+            if zero_pad:
+                assert bool((pad == 0).all()), f'group {i} padding not zeroed'
+            else:
+                assert bool((pad == SENTINEL).all()), f'group {i} padding touched'
+
+
+@pytest.mark.parametrize('n,k', [(512, 1024), (256, 2048)])
+def test_masked_vs_oracle(n, k):
+    g, max_m = 6, 256
+    x = gen.masked_inputs(g, max_m, n, k, seed=n + k)
+    print(f'masked masked_m={x["masked_m"].tolist()}', flush=True)
+    a_deq = np.stack([oquant.dequant_per_token(x['qa'][i], x['sfa'][i]) for i in range(g)])
+    b_deq = np.stack([oquant.dequant_per_block(x['qb'][i], x['sfb'][i]) for i in range(g)])
+    ref, valid = ogemm.gemm_masked(a_deq, b_deq, x['masked_m'])
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    mm = gen.to_dev(x['masked_m'])
+    d = sentinel_bf16((g, max_m, n))
+    deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, expected_m=128)
+    torch.cuda.synchronize()
+    out = d.float().cpu().numpy()
+    report('masked', out[valid], ref[valid])
+    assert ogemm.calc_diff(out[valid], ref[valid]) < 1e-3
+    assert bool((d.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
+    # each group equals a dense call on its valid rows
+    for i in range(g):
+        r = int(x['masked_m'][i])
+        dd = torch.empty((r, n), dtype=torch.bfloat16, device=DEV)
+        deep_gemm.fp8_gemm_nt((a[0][i, :r], a[1][i, :r]), (b[0][i], b[1][i]), dd)
+        assert torch.equal(dd.view(torch.int16), d[i, :r].view(torch.int16))
+
+
+def test_masked_edge_counts():
+    """masked_m of 0, 1, exactly max_m and a block boundary."""
+    g, max_m, n, k = 4, 256, 128, 256
+    x = gen.masked_inputs(g, max_m, n, k, seed=1)
+    x['masked_m'][:] = [0, 1, 256, 128]
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    d = sentinel_bf16((g, max_m, n))
+    deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, gen.to_dev(x['masked_m']), expected_m=64)
+    for i, r in enumerate(x['masked_m']):
+        assert bool((d[i, r:].view(torch.int16) == SENTINEL).all())
+        if r:
+            assert not bool((d[i, :r].view(torch.int16) == SENTINEL).any())
+
+
+# ----------------------------------------------------------------- SF layouts
+
+@pytest.mark.parametrize('mn,k,g', [(4096, 7168, 1), (4097, 128, 2), (300, 7296, 4)])
+def test_sf_transpose_and_pack(mn, k, g):
+    sfk = (k + 127) // 128
+    rng = np.random.default_rng(mn + k)
+    sf_np = rng.standard_normal((g, mn, sfk)).astype(np.float32)
+    sf = gen.to_dev(sf_np)
+    out = deep_gemm.get_mn_major_tma_aligned_tensor(sf)
+    amn = deep_gemm.get_tma_aligned_size(mn, 4)
+    assert out.stride() == (amn * sfk, 1, amn)
+    assert torch.equal(out, sf)
+    # transposed (non-contiguous) input takes the strided path
+    sf_t = sf.transpose(-1, -2).contiguous().transpose(-1, -2)
+    assert torch.equal(deep_gemm.get_mn_major_tma_aligned_tensor(sf_t), sf)
+    # UE8M0 packing, bitwise against the oracle's restatement of tests/test_layout.py:20-42
+    pow2 = np.ldexp(np.float32(1.0), rng.integers(-20, 20, size=(g, mn, sfk))).astype(np.float32)
+    packed = deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(gen.to_dev(pow2))
+    ref_storage = ogemm.pack_ue8m0_mn_major(pow2)       # [g, ceil(k/4), amn]
+    pk = (sfk + 3) // 4
+    assert packed.shape == (g, mn, pk) and packed.stride() == (amn * pk, 1, amn)
+    got = packed.cpu().numpy()
+    assert np.array_equal(got, np.swapaxes(ref_storage, 1, 2)[:, :mn, :])
+
+
+# ----------------------------------------------------------------- FP8 x FP4
+
+@pytest.mark.parametrize('m,n,k,a_fp4,gka', [(256, 384, 1024, False, 128), (100, 200, 512, False, 128),
+                                              (128, 256, 512, True, 32)])
+def test_fp8_fp4_vs_oracle(m, n, k, a_fp4, gka):
+    print(f'fp8xfp4 m={m} n={n} k={k} a_fp4={a_fp4}', flush=True)
+    x = gen.fp8_fp4_inputs(m, n, k, seed=m + k, gran_k_a=gka, gran_k_b=32, a_fp4=a_fp4)
+    a_deq = oquant.dequant_fp4(x['qa'], x['sfa'], gka) if a_fp4 else oquant.dequant_per_token(x['qa'], x['sfa'], gka)
+    ref = ogemm.gemm_nt(a_deq, oquant.dequant_fp4(x['qb'], x['sfb'], 32))
+    a_t = gen.to_dev(x['qa'], torch.int8) if a_fp4 else e4m3(x['qa'])
+    a = (a_t, f32(x['sfa']))
+    b = (gen.to_dev(x['qb'], torch.int8), f32(x['sfb']))
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, gka), recipe_b=(1, 32))
+    torch.cuda.synchronize()
+    out = d.float().cpu().numpy()
+    diff, rel = report('fp8xfp4', out, ref)
+    assert diff < 1e-5   # power-of-two scales: only BF16 output rounding remains
+    # packed-UE8M0 SFs give the same bits
+    pa = deep_gemm.transform_sf_into_required_layout(a[1], m, k, (1, gka))
+    pb = deep_gemm.transform_sf_into_required_layout(b[1], n, k, (1, 32))
+    assert pa.dtype == torch.int32 or gka == 128
+    d2 = torch.empty_like(d)
+    pa_i = deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(a[1])
+    deep_gemm.fp8_fp4_gemm_nt((a[0], pa_i), (b[0], pb), d2, recipe_a=(1, gka), recipe_b=(1, 32))
+    assert torch.equal(d.view(torch.int16), d2.view(torch.int16))
+
+
+# ----------------------------------------------------------------- quantizers
+
+def test_product_quantizers_match_oracle_on_gpu():
+    a = gen.randn_bf16((96, 1000), 31)
+    ta = torch.from_numpy(a).bfloat16().to(DEV)
+    q, s = deep_gemm.per_token_cast_to_fp8(ta, use_ue8m0=False)
+    oq, os_ = oquant.per_token_cast_to_fp8(a, use_ue8m0=False)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq) and np.array_equal(s.cpu().numpy(), os_)
+    q, s = deep_gemm.per_block_cast_to_fp8(ta, use_ue8m0=True)
+    oq, os_ = oquant.per_block_cast_to_fp8(a, use_ue8m0=True)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq) and np.array_equal(s.cpu().numpy(), os_)
+    q, s = deep_gemm.per_token_cast_to_fp4(ta, use_ue8m0=True, gran_k=32)
+    oq, os_ = oquant.per_token_cast_to_fp4(a, use_ue8m0=True, gran_k=32)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq) and np.array_equal(s.cpu().numpy(), os_)
