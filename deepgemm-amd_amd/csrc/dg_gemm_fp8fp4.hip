@@ -149,12 +149,16 @@ fp8_fp4_gemm_kernel(const Fp8Fp4GemmArgs p, const int num_m_blocks, const int nu
         else
             s_sb[st][tid - BM] = rs;
     };
-    // Operand of one 32x32x64 MFMA for row r, K step ks, lane half h:
-    // e4m3: 32 bytes = chunks 4ks+2h, 4ks+2h+1 of a 128-byte row;
-    // e2m1: 16 bytes = chunk 2ks+h of a 64-byte row (upper half unused).
+    // Operand of one 32x32x64 MFMA for row r, K step ks, lane half h. The scaled
+    // MFMA's K order within a 64-element step (measured on gfx950):
+    //   e2m1: lane half h holds K [32h, 32h+32) as 16 bytes (4 VGPRs, upper 4 unused)
+    //         -> chunk 2ks+h of a 64-byte row;
+    //   e4m3: lane half h holds K [16h, 16h+16) in bytes 0-15 and K [32+16h, 48+16h)
+    //         in bytes 16-31 -> chunks 4ks+h and 4ks+2+h of a 128-byte row.
+    // The E8M0 scale a lane supplies covers K block h = [32h, 32h+32) of the step.
     auto load_frag_fp8 = [&](const uint8_t* base, int r, int ks, int h) {
-        const i32x4 lo = *reinterpret_cast<const i32x4*>(base + swz<128>(r, ks * 4 + h * 2));
-        const i32x4 hi = *reinterpret_cast<const i32x4*>(base + swz<128>(r, ks * 4 + h * 2 + 1));
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(base + swz<128>(r, ks * 4 + h));
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(base + swz<128>(r, ks * 4 + 2 + h));
         return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
     auto load_frag_fp4 = [&](const uint8_t* base, int r, int ks, int h) {

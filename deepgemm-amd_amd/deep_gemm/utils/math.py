@@ -4,7 +4,8 @@ Same names, arguments and results as the reference's caller-side helpers
 (deep_gemm/utils/math.py:5-176): per-group amax clamped at 1e-4, scale =
 amax / 448 (FP8) or amax / 6 (FP4), optionally rounded up to a power of two
 (UE8M0), values multiplied by the float32 reciprocal of the scale and cast
-with round-to-nearest-even. They run wherever their input lives (on the GPU
+with round-to-nearest-even. The division by 448 / 6 is a multiplication by the
+float32 reciprocal, as torch evaluates it on the GPU, on every device. They run wherever their input lives (on the GPU
 for real workloads); they are not part of the GEMM kernels.
 """
 from typing import Tuple
@@ -49,7 +50,9 @@ def unpack_ue8m0_from_int(packed: torch.Tensor) -> torch.Tensor:
 
 
 def _group_scale(amax: torch.Tensor, max_code: float, use_ue8m0: bool) -> torch.Tensor:
-    sf = amax / max_code
+    # amax times the float32 reciprocal of the largest code: what `amax / max_code`
+    # evaluates to on the GPU, written so CPU tensors get the same bits.
+    sf = amax * (1.0 / max_code)
     return ceil_to_ue8m0(sf) if use_ue8m0 else sf
 
 

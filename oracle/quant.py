@@ -7,9 +7,16 @@ draws ``randn`` in bf16 before casting, ``tests/generators.py:357-358``). Every
 step is done in float32 with IEEE rounding, in the reference's order:
 
     amax = max|x| over the group, clamped below at 1e-4   (float32)
-    sf   = amax / 448           (or / 6 for FP4)          (float32 division)
+    sf   = amax * fl32(1 / 448) (or 1 / 6 for FP4)        (float32 product)
     sf   = ceil_to_ue8m0(sf)    when use_ue8m0
     q    = cast(x * (1 / sf))   (float32 reciprocal, float32 product, RNE cast)
+
+The reference writes ``sf = amax / 448.0`` and runs it on the GPU, where torch's
+division of a tensor by a Python scalar multiplies by the scalar's float32
+reciprocal (PyTorch's CUDA/ROCm true-divide kernel); that product, not the
+correctly rounded quotient, is what DeepGEMM's tests feed the GEMM (they differ
+by one ulp in a few percent of groups). The oracle restates the GPU behaviour;
+``tests/test_gemm_gpu.py::test_product_quantizers_match_oracle_on_gpu`` pins it.
 
 Functions and the reference lines they follow:
 
@@ -27,6 +34,10 @@ inputs, and bitwise agreement with torch's own float8_e4m3fn cast pipeline.
 import numpy as np
 
 from . import fp8
+
+
+_INV_E4M3_MAX = np.float32(1.0 / 448.0)   # fl32 of the reciprocal, as torch applies it
+_INV_E2M1_MAX = np.float32(1.0 / 6.0)
 
 
 def _align(x: int, y: int) -> int:
@@ -47,7 +58,7 @@ def per_token_cast_to_fp8(x: np.ndarray, use_ue8m0: bool, gran_k: int = 128):
     xp[:, :n] = x
     xv = xp.reshape(m, pn // gran_k, gran_k)
     amax = np.maximum(np.abs(xv).max(axis=2), np.float32(1e-4)).astype(np.float32)
-    sf = (amax / np.float32(448.0)).astype(np.float32)
+    sf = (amax * _INV_E4M3_MAX).astype(np.float32)
     if use_ue8m0:
         sf = fp8.ceil_to_ue8m0(sf)
     scaled = (xv * _recip_f32(sf)[:, :, None]).astype(np.float32)
@@ -65,7 +76,7 @@ def per_block_cast_to_fp8(x: np.ndarray, use_ue8m0: bool, gran_k: int = 128):
     xp[:m, :n] = x
     xv = xp.reshape(pm // gran_k, gran_k, pn // gran_k, gran_k)
     amax = np.maximum(np.abs(xv).max(axis=(1, 3)), np.float32(1e-4)).astype(np.float32)
-    sf = (amax / np.float32(448.0)).astype(np.float32)
+    sf = (amax * _INV_E4M3_MAX).astype(np.float32)
     if use_ue8m0:
         sf = fp8.ceil_to_ue8m0(sf)
     scaled = (xv * _recip_f32(sf)[:, None, :, None]).astype(np.float32)
@@ -83,7 +94,7 @@ def per_token_cast_to_fp4(x: np.ndarray, use_ue8m0: bool, gran_k: int = 128):
     xp[:, :n] = x
     xv = xp.reshape(m, pn // gran_k, gran_k)
     amax = np.maximum(np.abs(xv).max(axis=2), np.float32(1e-4)).astype(np.float32)
-    sf = (amax / np.float32(6.0)).astype(np.float32)
+    sf = (amax * _INV_E2M1_MAX).astype(np.float32)
     if use_ue8m0:
         sf = fp8.ceil_to_ue8m0(sf)
     scaled = (xv * _recip_f32(sf)[:, :, None]).astype(np.float32)

@@ -1,0 +1,224 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects malformed arguments on the host (before any HIP
+call) with the reference's error format."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import deep_gemm
+from deep_gemm import _ffi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'deepgemm_mi355x.h')
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(dg_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_header_symbols_exported():
+    syms = declared_symbols()
+    assert len(syms) >= 15
+    lib = ctypes.CDLL(_ffi.LIB_PATH)
+    for s in syms:
+        assert hasattr(lib, s), f'{s} declared in the header but not exported'
+    assert set(syms) == set(_ffi.SIGNATURES), 'binding table out of sync with the header'
+
+
+def test_version_and_init():
+    assert b'gfx950' in _ffi.lib.dg_version()
+    assert _ffi.lib.dg_init() == 0
+    assert _ffi.lib.dg_last_error() == b''
+
+
+def test_tma_aligned_size():
+    assert deep_gemm.get_tma_aligned_size(4097, 4) == 4100
+    assert deep_gemm.get_tma_aligned_size(4096, 4) == 4096
+    assert deep_gemm.get_tma_aligned_size(5, 1) == 16
+    with pytest.raises(RuntimeError, match='Assertion error'):
+        deep_gemm.get_tma_aligned_size(5, 3)
+
+
+def test_alignment_and_num_sms_knobs():
+    assert deep_gemm.get_mk_alignment_for_contiguous_layout() == 128
+    deep_gemm.set_mk_alignment_for_contiguous_layout(256)
+    assert deep_gemm.get_m_alignment_for_contiguous_layout() == 256
+    deep_gemm.set_mk_alignment_for_contiguous_layout(128)
+    assert deep_gemm.get_theoretical_mk_alignment_for_contiguous_layout() == 128
+    deep_gemm.set_num_sms(200)
+    assert deep_gemm.get_num_sms() == 200
+    deep_gemm.init()
+    with pytest.raises(RuntimeError):
+        deep_gemm.set_num_sms(0)
+    with pytest.raises(RuntimeError, match='Unsupported'):
+        deep_gemm.set_tile_override(96, 64)
+
+
+# ----------------------------------------------------------------- host validation
+# dg_tensor structs with device = 0 and fake addresses: every call below must be
+# rejected by a host check, before the library could touch device memory.
+
+def fake(shape, dtype, strides=None, addr=0x10000000, device=0):
+    t = _ffi.DgTensor()
+    t.data = addr
+    t.dtype = dtype
+    t.ndim = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    for i, (s, st) in enumerate(zip(shape, strides)):
+        t.sizes[i] = s
+        t.strides[i] = st
+    t.device = device
+    return t
+
+
+def call_nt(a, sfa, b, sfb, d, c=None, recipe=None, disable=0):
+    st = _ffi.lib.dg_fp8_fp4_gemm_nt(ctypes.byref(a), ctypes.byref(sfa), ctypes.byref(b), ctypes.byref(sfb),
+                                    ctypes.byref(d), ctypes.byref(c) if c else None,
+                                    ctypes.byref(recipe) if recipe else None, disable, None)
+    return st, _ffi.lib.dg_last_error().decode()
+
+
+def good_dense(m=256, n=512, k=1024):
+    return (fake((m, k), _ffi.DG_E4M3), fake((m, k // 128), _ffi.DG_F32), fake((n, k), _ffi.DG_E4M3),
+            fake((n // 128, k // 128), _ffi.DG_F32), fake((m, n), _ffi.DG_BF16))
+
+
+def test_rejects_host_tensors():
+    a, sfa, b, sfb, d = good_dense()
+    a.device = -1
+    st, msg = call_nt(a, sfa, b, sfb, d)
+    assert st == _ffi.DG_ERR_INVALID and 'on_device' in msg and msg.startswith('Assertion error (')
+
+
+def test_rejects_shape_mismatch():
+    a, sfa, b, sfb, _ = good_dense()
+    st, msg = call_nt(a, sfa, b, sfb, fake((256, 500), _ffi.DG_BF16))
+    assert st == _ffi.DG_ERR_INVALID and 'm == m_' in msg
+
+
+def test_rejects_mn_major_a():
+    m, k = 256, 1024
+    _, sfa, b, sfb, d = good_dense()
+    a = fake((m, k), _ffi.DG_E4M3, strides=(1, m))
+    st, msg = call_nt(a, sfa, b, sfb, d)
+    assert st == _ffi.DG_ERR_INVALID and 'is_k_major(a)' in msg
+
+
+def test_rejects_bad_output_dtype():
+    a, sfa, b, sfb, _ = good_dense()
+    st, msg = call_nt(a, sfa, b, sfb, fake((256, 512), _ffi.DG_F16))
+    assert st == _ffi.DG_ERR_INVALID and 'DG_BF16' in msg
+
+
+def test_rejects_bad_sf_shapes():
+    a, sfa, b, sfb, d = good_dense()
+    st, msg = call_nt(a, fake((256, 7), _ffi.DG_F32), b, sfb, d)
+    assert st == _ffi.DG_ERR_INVALID and 'sf.size(-1)' in msg
+    st, msg = call_nt(a, sfa, b, fake((3, 8), _ffi.DG_F32), d)
+    assert st == _ffi.DG_ERR_INVALID and 'sf.size(-2)' in msg
+
+
+def test_rejects_recipe_and_pair_together():
+    a, sfa, b, sfb, d = good_dense()
+    r = _ffi.recipe_struct((1, 128, 128))
+    r.has_recipe_ab = 1
+    st, msg = call_nt(a, sfa, b, sfb, d, recipe=r)
+    assert st == _ffi.DG_ERR_INVALID and 'has_recipe' in msg
+
+
+def test_rejects_c_dtype_mismatch():
+    a, sfa, b, sfb, _ = good_dense()
+    d = fake((256, 512), _ffi.DG_F32)
+    c = fake((256, 512), _ffi.DG_BF16, addr=0x20000000)
+    st, msg = call_nt(a, sfa, b, sfb, d, c=c)
+    assert st == _ffi.DG_ERR_INVALID and 'dtype' in msg
+
+
+def test_rejects_unaligned_operand():
+    a, sfa, b, sfb, d = good_dense()
+    a.data = 0x10000008
+    st, msg = call_nt(a, sfa, b, sfb, d)
+    assert st == _ffi.DG_ERR_INVALID and '16-byte aligned' in msg
+
+
+def test_unsupported_1d1d_fp32_recipe():
+    a, sfa, b, _, d = good_dense()
+    sfb = fake((512, 8), _ffi.DG_F32)
+    r = _ffi.recipe_struct(None, (1, 128), (1, 128))
+    st, msg = call_nt(a, sfa, b, sfb, d, recipe=r)
+    assert st == _ffi.DG_ERR_UNSUPPORTED and '1D1D' in msg
+
+
+def test_ue8m0_path_rejects_disable_cast():
+    m, n, k = 128, 256, 512
+    a = fake((m, k), _ffi.DG_E4M3)
+    sfa = fake((m, k // 128), _ffi.DG_F32)
+    b = fake((n, k // 2), _ffi.DG_I8)
+    sfb = fake((n, k // 32), _ffi.DG_F32)
+    d = fake((m, n), _ffi.DG_BF16)
+    r = _ffi.recipe_struct(None, (1, 128), (1, 32))
+    st, msg = call_nt(a, sfa, b, sfb, d, recipe=r, disable=1)
+    assert st == _ffi.DG_ERR_INVALID and 'disable_ue8m0_cast' in msg
+
+
+def test_grouped_validation():
+    g, m, n, k = 4, 512, 256, 1024
+    a = fake((m, k), _ffi.DG_E4M3)
+    sfa = fake((m, k // 128), _ffi.DG_F32)
+    b = fake((g, n, k), _ffi.DG_E4M3)
+    sfb = fake((g, n // 128, k // 128), _ffi.DG_F32)
+    d = fake((m, n), _ffi.DG_BF16)
+    idx = fake((m - 1,), _ffi.DG_I32)
+    st = _ffi.lib.dg_m_grouped_fp8_fp4_gemm_nt_contiguous(*(ctypes.byref(x) for x in (a, sfa, b, sfb, d, idx)),
+                                                          None, 0, 0, 1, -1, None)
+    assert st == _ffi.DG_ERR_INVALID and 'gl.size(0) == m' in _ffi.lib.dg_last_error().decode()
+    # masked: masked_m length must equal G
+    a3 = fake((g, 256, k), _ffi.DG_E4M3)
+    sfa3 = fake((g, 256, k // 128), _ffi.DG_F32)
+    d3 = fake((g, 256, n), _ffi.DG_BF16)
+    mm = fake((g + 1,), _ffi.DG_I32)
+    st = _ffi.lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(*(ctypes.byref(x) for x in (a3, sfa3, b, sfb, d3, mm)),
+                                                      128, None, 0, None)
+    assert st == _ffi.DG_ERR_INVALID and 'g == g___' in _ffi.lib.dg_last_error().decode()
+    # expected_m must be positive
+    mm = fake((g,), _ffi.DG_I32)
+    st = _ffi.lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(*(ctypes.byref(x) for x in (a3, sfa3, b, sfb, d3, mm)),
+                                                      0, None, 0, None)
+    assert st == _ffi.DG_ERR_INVALID and 'expected_m > 0' in _ffi.lib.dg_last_error().decode()
+
+
+def test_plan_sf_transform_kinds():
+    def plan(sf, mn, k, recipe3=None, recipe2=None, groups=-1, is_sfa=-1, disable=0):
+        kind = ctypes.c_int32(-1)
+        r3 = (ctypes.c_int32 * 3)(*recipe3) if recipe3 else None
+        r2 = (ctypes.c_int32 * 2)(*recipe2) if recipe2 else None
+        st = _ffi.lib.dg_plan_sf_transform(ctypes.byref(sf), mn, k, r3, r2, groups, is_sfa, disable,
+                                           ctypes.byref(kind))
+        return st, kind.value
+    assert plan(fake((4096, 56), _ffi.DG_F32), 4096, 7168, recipe3=(1, 128, 128), is_sfa=1) == (0, 1)
+    assert plan(fake((17, 56), _ffi.DG_F32), 2112, 7168, recipe3=(1, 128, 128), is_sfa=0) == (0, 0)
+    assert plan(fake((7168, 224), _ffi.DG_F32), 7168, 7168, recipe2=(1, 32)) == (0, 2)
+    st, _ = plan(fake((7168, 224), _ffi.DG_F32), 7168, 7168, recipe2=(1, 32), disable=1)
+    assert st == _ffi.DG_ERR_INVALID
+    st, _ = plan(fake((4096, 55), _ffi.DG_F32), 4096, 7168, recipe3=(1, 128, 128), is_sfa=1)
+    assert st == _ffi.DG_ERR_INVALID
+
+
+def test_python_shim_errors():
+    x = torch.zeros((128, 256), dtype=torch.float8_e4m3fn)
+    s = torch.ones((128, 2))
+    with pytest.raises(RuntimeError, match=r'Assertion error \(dg_api\.cpp:\d+\)'):
+        deep_gemm.fp8_gemm_nt((x, s), (x, torch.ones((1, 2))), torch.empty((128, 128), dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match='alpha'):
+        deep_gemm.fp8_gemm_nt((x, s), (x, s), torch.empty((128, 128)), alpha=2.0)
+    with pytest.raises(RuntimeError, match='epilogue'):
+        deep_gemm.fp8_gemm_nt((x, s), (x, s), torch.empty((128, 128)), epilogue=object())

@@ -354,3 +354,42 @@ def test_product_quantizers_match_oracle_on_gpu():
     q, s = deep_gemm.per_token_cast_to_fp4(ta, use_ue8m0=True, gran_k=32)
     oq, os_ = oquant.per_token_cast_to_fp4(a, use_ue8m0=True, gran_k=32)
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq) and np.array_equal(s.cpu().numpy(), os_)
+
+
+def test_fp8_ue8m0_gran32_vs_oracle():
+    """e4m3 x e4m3 with 1x32 power-of-two scales on both sides (scaled-MFMA path)."""
+    m, n, k = 192, 320, 768
+    a = gen.randn_bf16((m, k), 41)
+    b = gen.randn_bf16((n, k), 42)
+    qa, sfa = oquant.per_token_cast_to_fp8(a, use_ue8m0=True, gran_k=32)
+    qb, sfb = oquant.per_token_cast_to_fp8(b, use_ue8m0=True, gran_k=32)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(qa, sfa, 32), oquant.dequant_per_token(qb, sfb, 32))
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    deep_gemm.fp8_fp4_gemm_nt((e4m3(qa), f32(sfa)), (e4m3(qb), f32(sfb)), d, recipe_a=(1, 32), recipe_b=(1, 32))
+    diff, _ = report('fp8 ue8m0 gran32', d.float().cpu().numpy(), ref)
+    assert diff < 1e-5
+
+
+def test_fp8_fp4_masked_vs_oracle():
+    g, max_m, n, k = 4, 256, 256, 512
+    rng = np.random.default_rng(3)
+    masked = rng.integers(96, 161, size=g).astype(np.int32)
+    a = gen.randn_bf16((g, max_m, k), 51)
+    b = gen.randn_bf16((g, n, k), 52)
+    qa = np.empty((g, max_m, k), np.uint8)
+    sfa = np.empty((g, max_m, k // 128), np.float32)
+    qb = np.empty((g, n, k // 2), np.uint8)
+    sfb = np.empty((g, n, k // 32), np.float32)
+    for i in range(g):
+        qa[i], sfa[i] = oquant.per_token_cast_to_fp8(a[i], use_ue8m0=True)
+        qb[i], sfb[i] = oquant.per_token_cast_to_fp4(b[i], use_ue8m0=True, gran_k=32)
+    a_deq = np.stack([oquant.dequant_per_token(qa[i], sfa[i]) for i in range(g)])
+    b_deq = np.stack([oquant.dequant_fp4(qb[i], sfb[i], 32) for i in range(g)])
+    ref, valid = ogemm.gemm_masked(a_deq, b_deq, masked)
+    d = sentinel_bf16((g, max_m, n))
+    deep_gemm.m_grouped_fp8_fp4_gemm_nt_masked((e4m3(qa), f32(sfa)), (gen.to_dev(qb, torch.int8), f32(sfb)), d,
+                                               gen.to_dev(masked), 128, recipe_a=(1, 128), recipe_b=(1, 32))
+    out = d.float().cpu().numpy()
+    diff, _ = report('fp8xfp4 masked', out[valid], ref[valid])
+    assert diff < 1e-5
+    assert bool((d.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
