@@ -28,7 +28,7 @@ thread_local std::string t_last_config;
 constexpr int kDefaultMKAlignment = 128;
 std::atomic<int> g_num_sms{0};                 // 0: query the device
 std::atomic<int> g_mk_alignment{kDefaultMKAlignment};
-std::atomic<int> g_tile_m{0}, g_tile_n{0};     // 0: heuristic
+std::atomic<int> g_tile_variant{0}, g_tile_m{0}, g_tile_n{0};   // variant 0: heuristic
 
 template <typename F>
 int guarded(F&& f) {
@@ -247,31 +247,39 @@ const char* kind_name(GemmKind k) {
     return "?";
 }
 
-// Tile choice for the FP32-scale kernel. A tile shape's cost is the number of
-// rounds of resident workgroups it needs times the work of one tile divided
-// by that shape's relative MFMA efficiency (larger tiles re-read less LDS per
-// MFMA). Grouped kinds need block_m to divide the row alignment.
-TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t groups, int align_m) {
-    const int tm = g_tile_m.load(), tn = g_tile_n.load();
-    if (tm > 0 && tn > 0) {
-        if (!fp8_1d2d_tile_supported(tm, tn)) DG_UNSUPPORTED("tile override not compiled");
+// Tile choice for the FP32-scale kernels. A candidate's cost is the number of
+// rounds of resident workgroups it needs times the work of one tile divided by
+// that candidate's relative throughput (measured MFMA efficiency of the tile
+// shape and pipeline). Grouped kinds need block_m to divide the row alignment.
+TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k, int64_t groups, int align_m) {
+    const int tv = g_tile_variant.load(), tm = g_tile_m.load(), tn = g_tile_n.load();
+    // The pipelined kernel keeps one SFB value per K block in LDS (up to 1024 blocks).
+    const bool pipe_ok = ceil_div(k, 128) <= 1024;
+    if (tv > 0) {
+        const bool ok = tv == 1 ? fp8_1d2d_tile_supported(tm, tn) : (pipe_ok && fp8_1d2d_v2_tile_supported(tm, tn));
+        if (!ok) DG_UNSUPPORTED("tile override not compiled");
         if ((kind == kContiguous || kind == kPsum) && align_m % tm != 0)
             DG_UNSUPPORTED("tile override block_m must divide the M alignment");
-        return {tm, tn};
+        return {tm, tn, tv};
     }
-    struct Cand { int bm, bn, per_cu; double eff; };
-    static const Cand cands[] = {{128, 128, 2, 1.00}, {128, 64, 3, 0.80}, {64, 128, 3, 0.80}, {64, 64, 4, 0.62}};
+    struct Cand { int variant, bm, bn, per_cu; double eff; };
+    // Relative per-CU throughput of each kernel/tile, measured on MI355X at
+    // M = 4096 over the DeepSeek-V3 shapes (pipelined 256 x 128 = 1.0).
+    static const Cand cands[] = {
+        {2, 256, 128, 1, 1.00}, {2, 128, 256, 1, 0.97}, {2, 128, 128, 1, 0.80},
+        {1, 128, 128, 2, 0.80}, {1, 128, 64, 3, 0.55}, {1, 64, 128, 3, 0.55}, {1, 64, 64, 4, 0.45}};
     int cus = 256;
     try { cus = num_sms_now(); } catch (const Error&) {}
     double best = 1e300;
-    TileConfig out{64, 64};
+    TileConfig out{64, 64, 1};
     for (const auto& c : cands) {
         if ((kind == kContiguous || kind == kPsum) && align_m % c.bm != 0) continue;
+        if (c.variant == 2 && !pipe_ok) continue;
         const int64_t tiles = ceil_div(m_rows, c.bm) * ceil_div(n, c.bn) * groups;
         const int64_t slots = (int64_t)cus * c.per_cu;
         const double rounds = (double)ceil_div(tiles, slots);
         const double cost = rounds * c.bm * c.bn / c.eff / c.per_cu;
-        if (cost < best - 1e-9) best = cost, out = {c.bm, c.bn};
+        if (cost < best - 1e-9) best = cost, out = {c.bm, c.bn, c.variant};
     }
     return out;
 }
@@ -279,8 +287,9 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t gr
 void record_config(const char* kernel, GemmKind kind, const TileConfig& t, int64_t m, int64_t n, int64_t k,
                    int64_t g) {
     char buf[256];
-    std::snprintf(buf, sizeof(buf), "%s kind=%s block_m=%d block_n=%d m=%lld n=%lld k=%lld groups=%lld", kernel,
-                  kind_name(kind), t.block_m, t.block_n, (long long)m, (long long)n, (long long)k, (long long)g);
+    std::snprintf(buf, sizeof(buf), "%s v%d kind=%s block_m=%d block_n=%d m=%lld n=%lld k=%lld groups=%lld", kernel,
+                  t.variant, kind_name(kind), t.block_m, t.block_n, (long long)m, (long long)n, (long long)k,
+                  (long long)g);
     t_last_config = buf;
 }
 
@@ -343,11 +352,14 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
         args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
         const int64_t m_rows = m;
-        const TileConfig t = choose_tile_1d2d(kind, m_rows, n, kind == kMasked ? groups : 1, align_m);
+        const TileConfig t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
         if ((kind == kContiguous || kind == kPsum) && align_m % t.block_m != 0)
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
-        launch_fp8_gemm_1d2d(kind, t, args, stream);
+        if (t.variant == 2)
+            launch_fp8_gemm_1d2d_v2(kind, t, args, stream);
+        else
+            launch_fp8_gemm_1d2d(kind, t, args, stream);
         return;
     }
 
@@ -389,7 +401,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
         args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
         args.sfb_row_shift = r.gran_mn_b == 128 ? 7 : 0;
-        const TileConfig t{128, 128};
+        const TileConfig t{128, 128, 1};
         if ((kind == kContiguous || kind == kPsum) && align_m % t.block_m != 0)
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 128 on the UE8M0 path");
         record_config("fp8_fp4_gemm_ue8m0", kind, t, m, n, k, groups);
@@ -586,6 +598,7 @@ int dg_init(void) {
     return guarded([] {
         g_num_sms = 0;
         g_mk_alignment = kDefaultMKAlignment;
+        g_tile_variant = 0;
         g_tile_m = 0;
         g_tile_n = 0;
     });
@@ -676,14 +689,17 @@ int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m
     return kDefaultMKAlignment;
 }
 
-int dg_set_tile_override(int32_t block_m, int32_t block_n) {
+int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
     return guarded([&] {
-        if (block_m == 0 && block_n == 0) {
-            g_tile_m = 0, g_tile_n = 0;
+        if (variant == 0) {
+            g_tile_variant = 0, g_tile_m = 0, g_tile_n = 0;
             return;
         }
-        if (!fp8_1d2d_tile_supported(block_m, block_n)) DG_UNSUPPORTED("tile shape not compiled");
+        const bool ok = variant == 1 ? fp8_1d2d_tile_supported(block_m, block_n)
+                                     : (variant == 2 && fp8_1d2d_v2_tile_supported(block_m, block_n));
+        if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;
+        g_tile_variant = variant;
     });
 }
 

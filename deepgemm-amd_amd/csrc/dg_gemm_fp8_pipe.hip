@@ -1,0 +1,354 @@
+// Pipelined FP32-scale FP8 GEMM for gfx950 (the large-tile path).
+//
+// Same arithmetic as dg_gemm_fp8.hip — per 128-wide K block, a fresh FP32 matrix-
+// core accumulator promoted with fma(sa * sb, acc, final), as in the reference's
+// 1D2D kernel (deep_gemm/include/deep_gemm/impls/sm90_fp8_gemm_1d2d.cuh:281-345) —
+// with a deeper memory pipeline and larger wave tiles:
+//
+//  * v_mfma_f32_32x32x64_f8f6f4, two per 128-wide scale block, then 16 FMAs promote
+//    the 32 x 32 result. Measured on gfx950 this MFMA shape keeps ~97% of its peak
+//    with the promotion FMAs interleaved (the 16x16x128 shape keeps ~60%). Two
+//    accumulator sets alternate so one tile's MFMAs run while the previous tile's
+//    result is promoted.
+//  * Global tiles go straight to LDS with global_load_lds_dwordx4 (16 bytes per
+//    lane, 1 KB per wave instruction, no staging registers) into a STAGES-deep
+//    ring; loads for K block kb + STAGES - 1 are issued while kb computes. The
+//    loads are inline asm so the compiler adds no waits of its own (it would
+//    drain the whole ring before every LDS read). One
+//    plain s_barrier per K block, after an s_waitcnt that retires this wave's
+//    loads for kb: once every wave passes it, the stage is complete and every
+//    wave has consumed the slot about to be refilled. (The usual __syncthreads()
+//    also drains every later stage's loads, which would serialize the ring.)
+//  * LDS rows are 128 bytes; 16-byte chunk c of row r sits at c ^ g(r) with
+//    g(r) = ((r >> 1) ^ ((r & 1) << 2)) & 7: 16 consecutive rows at one logical
+//    chunk hit distinct banks for 8- and 16-lane LDS phases alike. A lane of the
+//    direct load owns a fixed physical slot and fetches the chunk that belongs there.
+//  * Interior tiles (all rows in range, K a multiple of 128) address every load
+//    as a wave-uniform SGPR base plus one per-lane 32-bit offset; edge tiles
+//    check rows and K chunks and send out-of-range lanes to a zero page.
+//  * The block's SFB values for all K blocks are loaded into LDS once, so the
+//    main loop issues no vector memory reads besides the stage loads.
+//  * 4 waves in a WGM x WGN grid; wave tile 128 x 64 (or 64 x 64) of 32 x 32
+//    MFMA tiles, large enough that LDS reads stay within the ~128 B/clk/CU the
+//    LDS delivers. The MFMA "A" operand is the weight tile, so a lane's
+//    accumulator column is one token row m (one sfa per lane).
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "dg_internal.hpp"
+#include "dg_kernel_common.hpp"
+
+namespace dgm {
+namespace {
+
+using namespace dev;
+
+constexpr int kBK = 128;
+constexpr int kMaxKBlocks = 1024;   // K up to 131072 on this path (the host routes longer K elsewhere)
+
+// Source for lanes whose row or K chunk is out of range.
+__device__ __attribute__((aligned(16))) uint8_t g_zero_page[16] = {0};
+
+__device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+__device__ __forceinline__ int swz16(int r, int c) { return r * 128 + ((c ^ swz_g(r)) << 4); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<size_t>((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+// Direct global -> LDS loads, written as inline asm so that the compiler does
+// not track them: its LDS-DMA alias analysis cannot tell the ring's stages
+// apart and would drain every in-flight stage before each LDS read. The kernel
+// orders them itself with s_waitcnt vmcnt + s_barrier. Each wave instruction
+// writes lds + lane * size; M0 holds the wave-uniform LDS base (M0 is not
+// otherwise live in these kernels).
+__device__ __forceinline__ void dma16_saddr(const uint8_t* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_saddr(const uint8_t* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_vaddr(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_vaddr(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
+                 : "memory", "m0");
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C>
+__global__ void __launch_bounds__(kThreads, 1)
+fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int num_n_blocks) {
+    static_assert(WGM * WGN == 4, "4 waves");
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int SM = WM / 32, SN = WN / 32;
+    constexpr int A_INSTR = BM / 32;          // 1 KB wave loads per stage for A (4 waves x A_INSTR x 1 KB)
+    constexpr int B_INSTR = BN / 32;
+    constexpr int LOADS_PER_STAGE = A_INSTR + B_INSTR + 1;   // + one SFA load
+    constexpr int SA_OFF = (BM + BN) * kBK;
+    constexpr int SA_ROWS_PER_WAVE = BM / 4;  // SFA rows loaded by each wave (<= 64)
+    constexpr int STAGE_BYTES = SA_OFF + 4 * 256;
+    static_assert(WN <= 128 && 128 % WN == 0, "a wave's N range must sit in one 128-row SFB block");
+    static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
+    static_assert((STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
+
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
+    __shared__ float s_sfb[2][kMaxKBlocks];   // SFB of the block's (at most two) 128-row N groups
+    __shared__ int s_flag;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    const Tile t = decode_tile<BM, BN, KIND>(p.m, p.n, p.num_groups, p.layout, p.align_m, p.zero_padding,
+                                             num_m_blocks, num_n_blocks, static_cast<uint16_t*>(p.d), p.ldd,
+                                             &s_flag);
+    if (!t.active) return;
+    const int m0 = t.m0, n0 = t.n0;
+
+    const uint8_t* __restrict__ a_base =
+        p.a + ((KIND == kMasked) ? (int64_t)t.g * p.a_gs : 0) + (int64_t)m0 * p.lda;
+    const uint8_t* __restrict__ b_base = p.b + (int64_t)t.expert * p.b_gs + (int64_t)n0 * p.ldb;
+    const float* __restrict__ sa_base =
+        p.sfa + ((KIND == kMasked) ? (int64_t)t.g * p.sfa_gs : 0) + (int64_t)m0 * p.sfa_sm;
+
+    const int a_rows = min(BM, t.row_end - m0);
+    const int b_rows = min(BN, p.n - n0);
+    const int num_kb = (p.k + kBK - 1) / kBK;
+
+    {
+        const float* sfb_g = p.sfb + (int64_t)t.expert * p.sfb_gs;
+        const int last_row = (p.n - 1) >> 7;
+        for (int idx = tid; idx < 2 * num_kb; idx += kThreads) {
+            const int gsel = idx / num_kb, kb = idx % num_kb;
+            const int row = min((n0 >> 7) + gsel, last_row);
+            s_sfb[gsel][kb] = sfb_g[(int64_t)row * p.sfb_sn + (int64_t)kb * p.sfb_sk];
+        }
+    }
+    __syncthreads();   // s_sfb visible; no stage loads are in flight yet
+    const int my_group = (wn * WN) >> 7;
+
+    const int lrow = lane & 31;
+    const int lhalf = lane >> 5;
+    const int rs = lane >> 3, pc = lane & 7;   // row and physical chunk a lane owns in a 1 KB load segment
+
+    f32x16 fin[SM][SN];
+#pragma unroll
+    for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) fin[i][j][e] = 0.f;
+
+    // 32 consecutive K bytes (chunks c, c+1) of row r of an LDS tile.
+    auto frag = [&](const uint8_t* tile, int r, int c) {
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(tile + swz16(r, c));
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(tile + swz16(r, c + 1));
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    auto compute = [&](int kb) {
+        const uint8_t* sbase = smem + (kb % STAGES) * STAGE_BYTES;
+        const uint8_t* a_tile = sbase;
+        const uint8_t* b_tile = sbase + BM * kBK;
+        const float sb = s_sfb[my_group][kb];
+        float sa[SM];
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+            const int r = wm * WM + i * 32 + lrow;
+            sa[i] = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
+                                                    (r % SA_ROWS_PER_WAVE) * 4) * sb;
+        }
+        i32x8 op_n[SN][2];
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) op_n[j][ks] = frag(b_tile, wn * WN + j * 32 + lrow, ks * 4 + lhalf * 2);
+
+        // Tiles in order t = i * SN + j; acc[t & 1] holds tile t while tile t - 1 is promoted.
+        f32x16 acc[2];
+        i32x8 om0 = frag(a_tile, wm * WM + lrow, lhalf * 2);
+        i32x8 om1 = frag(a_tile, wm * WM + lrow, 4 + lhalf * 2);
+#pragma unroll
+        for (int tt = 0; tt <= SM * SN; ++tt) {
+            if (tt < SM * SN) {
+                const int i = tt / SN, j = tt % SN;
+                if (j == 0 && i > 0) {
+                    om0 = frag(a_tile, wm * WM + i * 32 + lrow, lhalf * 2);
+                    om1 = frag(a_tile, wm * WM + i * 32 + lrow, 4 + lhalf * 2);
+                }
+                f32x16 c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op_n[j][0], om0, f32x16{}, 0, 0, 0, 0, 0,
+                                                                           0);
+                acc[tt & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op_n[j][1], om1, c, 0, 0, 0, 0, 0, 0);
+            }
+            if (tt > 0) {
+                const int pt = tt - 1, i = pt / SN, j = pt % SN;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) fin[i][j][e] = __builtin_fmaf(sa[i], acc[pt & 1][e], fin[i][j][e]);
+            }
+        }
+    };
+
+    auto mainloop = [&](auto bounds_tag) {
+        constexpr bool BOUNDS = decltype(bounds_tag)::value;
+        // Interior: one per-lane offset per operand. Segment s covers rows 8s..8s+7 and
+        // s = i*4 + wave, so the swizzle phase (bit 3 of the row) is wave & 1 for all s.
+        const uint32_t voff_a = rs * (uint32_t)p.lda + ((pc ^ swz_g((wave & 1) * 8 + rs)) << 4);
+        const uint32_t voff_b = rs * (uint32_t)p.ldb + ((pc ^ swz_g((wave & 1) * 8 + rs)) << 4);
+        const int sa_row = wave * SA_ROWS_PER_WAVE + lane;
+        const uint32_t voff_sa = lane < SA_ROWS_PER_WAVE ? (uint32_t)(sa_row * p.sfa_sm) * 4u : 0u;
+
+        const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
+        auto issue_stage = [&](int kb, int st) {
+            const uint32_t stage_lds = smem_lds + st * STAGE_BYTES;
+            if constexpr (!BOUNDS) {
+                const uint8_t* a_kb = a_base + kb * kBK;
+                const uint8_t* b_kb = b_base + kb * kBK;
+#pragma unroll
+                for (int i = 0; i < A_INSTR; ++i) {
+                    const int seg = i * 4 + wave;
+                    dma16_saddr(a_kb + (int64_t)seg * 8 * p.lda, voff_a, stage_lds + seg * 1024);
+                }
+#pragma unroll
+                for (int i = 0; i < B_INSTR; ++i) {
+                    const int seg = i * 4 + wave;
+                    dma16_saddr(b_kb + (int64_t)seg * 8 * p.ldb, voff_b, stage_lds + BM * kBK + seg * 1024);
+                }
+                dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
+                           stage_lds + SA_OFF + wave * 256);
+            } else {
+#pragma unroll
+                for (int i = 0; i < A_INSTR; ++i) {
+                    const int seg = i * 4 + wave;
+                    const int r = seg * 8 + rs;
+                    const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
+                    const void* src = (r < a_rows && k < p.k) ? (const void*)(a_base + (int64_t)r * p.lda + k)
+                                                              : (const void*)g_zero_page;
+                    dma16_vaddr(src, stage_lds + seg * 1024);
+                }
+#pragma unroll
+                for (int i = 0; i < B_INSTR; ++i) {
+                    const int seg = i * 4 + wave;
+                    const int r = seg * 8 + rs;
+                    const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
+                    const void* src = (r < b_rows && k < p.k) ? (const void*)(b_base + (int64_t)r * p.ldb + k)
+                                                              : (const void*)g_zero_page;
+                    dma16_vaddr(src, stage_lds + BM * kBK + seg * 1024);
+                }
+                const void* src = (lane < SA_ROWS_PER_WAVE && sa_row < a_rows)
+                                      ? (const void*)(sa_base + (int64_t)sa_row * p.sfa_sm + (int64_t)kb * p.sfa_sk)
+                                      : (const void*)g_zero_page;
+                dma4_vaddr(src, stage_lds + SA_OFF + wave * 256);
+            }
+        };
+
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s)
+            if (s < num_kb) issue_stage(s, s);
+
+        for (int kb = 0; kb < num_kb; ++kb) {
+            // Loads for kb are complete once at most (STAGES - 2) later stages remain in flight.
+            if (kb + STAGES - 2 < num_kb)
+                wait_vmcnt_barrier<(STAGES - 2) * LOADS_PER_STAGE>();
+            else
+                wait_vmcnt_barrier<0>();
+            if (kb + STAGES - 1 < num_kb) issue_stage(kb + STAGES - 1, (kb + STAGES - 1) % STAGES);
+            compute(kb);
+        }
+    };
+
+    const bool interior = a_rows == BM && b_rows == BN && (p.k % kBK) == 0;
+    if (interior)
+        mainloop(std::false_type{});
+    else
+        mainloop(std::true_type{});
+
+    // Epilogue: lane owns column m of each 32x32 tile; registers 4q..4q+3 are
+    // rows n = 8q + 4*lhalf + 0..3 of that tile.
+    const int64_t d_goff = (KIND == kMasked) ? (int64_t)t.g * p.d_gs : 0;
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+        const int m = m0 + wm * WM + i * 32 + lrow;
+        bool store, zero;
+        row_predicate<KIND>(t, p.m, p.layout, m, store, zero);
+        if (!store && !zero) continue;
+#pragma unroll
+        for (int j = 0; j < SN; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wn * WN + j * 32 + q * 8 + lhalf * 4;
+                if (n >= p.n) continue;
+                const f32x16& f = fin[i][j];
+                store4<OUT_F32, HAS_C>(p.d, p.c, d_goff + (int64_t)m * p.ldd + n, (int64_t)m * p.ldc + n, n, p.n,
+                                       zero ? 0.f : f[q * 4 + 0], zero ? 0.f : f[q * 4 + 1],
+                                       zero ? 0.f : f[q * 4 + 2], zero ? 0.f : f[q * 4 + 3]);
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND>
+void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
+    const int num_n_blocks = (a.n + BN - 1) / BN;
+    const int num_m_blocks = (a.m + BM - 1) / BM;
+    int64_t grid = (int64_t)num_m_blocks * num_n_blocks;
+    if (KIND == kMasked) grid *= a.num_groups;
+    if (grid == 0) return;
+    DG_CHECK(grid < (int64_t)1 << 31);
+    DG_CHECK((a.k + kBK - 1) / kBK <= kMaxKBlocks);
+    const dim3 gdim(static_cast<unsigned>(grid)), bdim(kThreads);
+#define DG_PIPE_LAUNCH(OF, HC)                                                                                   \
+    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC>), gdim, bdim, 0, stream, \
+                       a, num_m_blocks, num_n_blocks)
+    if constexpr (KIND != kNormal) {
+        DG_CHECK(!a.out_f32 && a.c == nullptr);
+        DG_PIPE_LAUNCH(0, 0);
+    } else if (a.out_f32) {
+        if (a.c) DG_PIPE_LAUNCH(1, 1); else DG_PIPE_LAUNCH(1, 0);
+    } else {
+        if (a.c) DG_PIPE_LAUNCH(0, 1); else DG_PIPE_LAUNCH(0, 0);
+    }
+#undef DG_PIPE_LAUNCH
+    DG_HIP_CHECK(hipGetLastError());
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES>
+void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
+    switch (kind) {
+        case kNormal: launch_kind<BM, BN, WGM, WGN, STAGES, kNormal>(a, stream); break;
+        case kContiguous: launch_kind<BM, BN, WGM, WGN, STAGES, kContiguous>(a, stream); break;
+        case kMasked: launch_kind<BM, BN, WGM, WGN, STAGES, kMasked>(a, stream); break;
+        case kPsum: launch_kind<BM, BN, WGM, WGN, STAGES, kPsum>(a, stream); break;
+        default: DG_UNSUPPORTED("unknown GEMM kind");
+    }
+}
+
+}  // namespace
+
+bool fp8_1d2d_v2_tile_supported(int bm, int bn) {
+    return (bm == 256 && bn == 128) || (bm == 128 && bn == 256) || (bm == 128 && bn == 128);
+}
+
+void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args, hipStream_t stream) {
+    const int key = cfg.block_m * 1000 + cfg.block_n;
+    switch (key) {
+        case 256128: launch_tile<256, 128, 2, 2, 3>(kind, args, stream); break;   // waves 128 x 64
+        case 128256: launch_tile<128, 256, 1, 4, 3>(kind, args, stream); break;   // waves 128 x 64
+        case 128128: launch_tile<128, 128, 2, 2, 4>(kind, args, stream); break;   // waves 64 x 64
+        default: DG_UNSUPPORTED("tile shape not compiled for the pipelined FP32-scale FP8 kernel");
+    }
+}
+
+}  // namespace dgm

@@ -80,6 +80,7 @@ struct Fp8GemmArgs {
 struct TileConfig {
     int block_m;
     int block_n;
+    int variant = 1;   // FP32-scale kernels: 1 = register-staged 32x32x64, 2 = LDS-pipelined 16x16x128
 };
 
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
@@ -89,6 +90,11 @@ void launch_fp8_gemm_1d2d(GemmKind kind, const TileConfig& cfg, const Fp8GemmArg
 
 // Tile shapes compiled for the FP32-scale kernel (block_m, block_n).
 bool fp8_1d2d_tile_supported(int block_m, int block_n);
+
+// The LDS-pipelined FP32-scale kernel (dg_gemm_fp8_v2.hip).
+void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args,
+                             hipStream_t stream);
+bool fp8_1d2d_v2_tile_supported(int block_m, int block_n);
 
 // Arguments of the UE8M0 block-scaled kernel (A e4m3 or e2m1, B e4m3 or e2m1,
 // scales applied inside the scaled MFMA).

@@ -297,9 +297,11 @@ def transform_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe,
 
 # ------------------------------------------------------------------ introspection
 
-def set_tile_override(block_m: int = 0, block_n: int = 0) -> None:
-    """Force the FP32-scale kernel's tile (0, 0 = heuristic). Testing/tuning aid."""
-    _check(_lib.dg_set_tile_override(int(block_m), int(block_n)))
+def set_tile_override(block_m: int = 0, block_n: int = 0, variant: int = 2) -> None:
+    """Force the FP32-scale kernel variant and tile ((0, 0) = heuristic). Testing/tuning aid."""
+    if block_m == 0 and block_n == 0:
+        variant = 0
+    _check(_lib.dg_set_tile_override(int(variant), int(block_m), int(block_n)))
 
 
 def get_last_config() -> str:

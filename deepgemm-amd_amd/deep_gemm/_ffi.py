@@ -76,7 +76,7 @@ SIGNATURES = {
     'dg_set_mk_alignment_for_contiguous_layout': (_I, [_I]),
     'dg_get_mk_alignment_for_contiguous_layout': (_I, []),
     'dg_get_theoretical_mk_alignment_for_contiguous_layout': (_I, [_I]),
-    'dg_set_tile_override': (_I, [_I, _I]),
+    'dg_set_tile_override': (_I, [_I, _I, _I]),
     'dg_last_config': (_I, [ctypes.c_char_p, _I]),
 }
 

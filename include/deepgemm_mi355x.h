@@ -194,10 +194,12 @@ int dg_set_mk_alignment_for_contiguous_layout(int32_t alignment);
 int32_t dg_get_mk_alignment_for_contiguous_layout(void);
 int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m);
 
-/* Tile override for tests and tuning (no reference counterpart; the reference's
- * closest knob is DG_JIT_* config printing). block_m = block_n = 0 restores the
- * heuristic. Only listed tile shapes are accepted. */
-int dg_set_tile_override(int32_t block_m, int32_t block_n);
+/* Kernel/tile override for tests and tuning (no reference counterpart; the
+ * reference's closest knobs are its JIT config printing and
+ * set_block_size_multiple_of, csrc/apis/config.hpp:40-47). variant 1 = the
+ * register-staged 32x32x64 kernel, 2 = the LDS-pipelined 16x16x128 kernel;
+ * variant 0 restores the heuristic. Only compiled tile shapes are accepted. */
+int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n);
 
 /* Describes the kernel configuration the last GEMM call on this thread chose
  * (reference: DG_PRINT_CONFIGS, csrc/jit_kernels/heuristics/common.hpp:44-54).

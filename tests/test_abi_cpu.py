@@ -56,7 +56,9 @@ def test_alignment_and_num_sms_knobs():
     with pytest.raises(RuntimeError):
         deep_gemm.set_num_sms(0)
     with pytest.raises(RuntimeError, match='Unsupported'):
-        deep_gemm.set_tile_override(96, 64)
+        deep_gemm.set_tile_override(96, 64, variant=1)
+    with pytest.raises(RuntimeError, match='Unsupported'):
+        deep_gemm.set_tile_override(64, 64, variant=2)
 
 
 # ----------------------------------------------------------------- host validation

@@ -84,16 +84,19 @@ def test_all_tiles_bitwise_equal():
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
     outs = []
     try:
-        for bm, bn in ((64, 64), (64, 128), (128, 64), (128, 128)):
-            deep_gemm.set_tile_override(bm, bn)
+        for v, bm, bn in ((1, 64, 64), (1, 64, 128), (1, 128, 64), (1, 128, 128),
+                          (2, 128, 128), (2, 128, 256), (2, 256, 128)):
+            deep_gemm.set_tile_override(bm, bn, variant=v)
             d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
             deep_gemm.fp8_gemm_nt(a, b, d)
-            outs.append(d)
+            outs.append((v, d))
             print(deep_gemm.get_last_config(), flush=True)
     finally:
         deep_gemm.set_tile_override(0, 0)
-    for o in outs[1:]:
-        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    # both variants use the same MFMA shape and per-K-block order, so every tile
+    # shape of either kernel gives the same bits
+    for _, o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0][1].view(torch.int16))
 
 
 @pytest.mark.parametrize('inplace', [True, False])
