@@ -278,7 +278,9 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
         const int64_t tiles = ceil_div(m_rows, c.bm) * ceil_div(n, c.bn) * groups;
         const int64_t slots = (int64_t)cus * c.per_cu;
         const double rounds = (double)ceil_div(tiles, slots);
-        const double cost = rounds * c.bm * c.bn / c.eff / c.per_cu;
+        // One round runs per_cu tiles on every CU at once: its time is the work of
+        // per_cu tiles at the candidate's throughput.
+        const double cost = rounds * c.bm * c.bn * c.per_cu / c.eff;
         if (cost < best - 1e-9) best = cost, out = {c.bm, c.bn, c.variant};
     }
     return out;
