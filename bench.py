@@ -27,6 +27,11 @@ PEAK_FP8_TFLOPS = 5000.0     # MI355X dense FP8 MFMA (AMD public spec: 2.5 PFLOP
 PEAK_FP4_TFLOPS = 10100.0
 PEAK_HBM_GBS = 8000.0
 DENSE_NK = [(2112, 7168), (24576, 1536), (7168, 16384), (4096, 7168), (7168, 2048)]
+# Calibrated HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
+# written by deep_gemm.testing.rocprof_summary), per workload.
+PROFILE_NAMES = {'dense': 'fp8_gemm_nt_dense_m4096', 'dense_acc': 'fp8_gemm_nt_dense_acc_m4096',
+                 'contiguous': 'm_grouped_fp8_gemm_nt_contiguous_e8_t32768',
+                 'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096'}
 
 
 def parse():
@@ -38,6 +43,9 @@ def parse():
                     choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--cpu-sample-m', type=int, default=512)
+    ap.add_argument('--calibrate-copy-mib', type=int, default=0,
+                    help='first run torch.neg over this many MiB of float32 (a plain copy kernel of known '
+                         'size, the reference for FETCH_SIZE / WRITE_SIZE counter passes)')
     return ap.parse_args()
 
 
@@ -204,6 +212,22 @@ def cpu_baseline(workload: str, sample_m: int):
                       f'FP32 matmul (numpy BLAS, {cores} host threads), one pass, {secs:.1f} s total'}
 
 
+def load_traffic(workload, launches, configs):
+    """Calibrated HBM bytes of one step from the committed counter summary,
+    used only when every launch ran the kernel configuration it was measured on."""
+    path = os.path.join(ROOT, 'profiles', PROFILE_NAMES[workload] + '.json')
+    if not os.path.exists(path):
+        return None, 'no counter summary for this workload'
+    rec = json.load(open(path))
+    per = rec.get('per_launch_bytes')
+    if not per:
+        return None, f'{os.path.basename(path)} holds no traffic figures'
+    for l, c in zip(launches, configs):
+        if rec.get('launch_config', {}).get(l.name) != c or l.name not in per:
+            return None, f'{os.path.basename(path)} was measured on another kernel configuration'
+    return sum(per[l.name]['total'] for l in launches), f'profiles/{os.path.basename(path)}'
+
+
 # ---------------------------------------------------------------- main
 
 def main():
@@ -217,6 +241,13 @@ def main():
     torch.cuda.set_device(0)
     makers = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
               'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4}
+    if args.calibrate_copy_mib > 0:
+        x = torch.randn(args.calibrate_copy_mib * 1024 * 256, device='cuda:0')
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.neg(x, out=y)
+        torch.cuda.synchronize()
+        del x, y
     launches, cfg, bound = makers[args.workload]()
     torch.cuda.synchronize()
     log(f'workload {args.workload}: {len(launches)} launches per step')
@@ -229,7 +260,7 @@ def main():
     # Per-launch durations, HIP events on the launch stream (torch's current stream,
     # which the library launches on), back-to-back repetitions of each launch.
     stream = torch.cuda.current_stream()
-    per = []
+    per, configs = [], []
     for l in launches:
         reps = max(5, args.steps)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -240,6 +271,7 @@ def main():
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / reps
         per.append(us)
+        configs.append(deep_gemm.get_last_config())
         log(f'  {l.name}: {us:8.1f} us  {l.flops / us / 1e6:7.1f} TFLOPS  {l.nbytes / us / 1e3:7.1f} GB/s  '
             f'[{deep_gemm.get_last_config()}]')
 
@@ -264,9 +296,16 @@ def main():
         peak = PEAK_HBM_GBS
         achieved = total_bytes / kernel_us / 1e3
         unit = 'GB/s'
+    traffic, traffic_note = load_traffic(args.workload, launches, configs)
     roofline = {'bound': bound, 'achieved': round(achieved, 2), 'peak': peak, 'unit': unit,
-                'frac': round(achieved / peak, 4), 'traffic': None,
-                'kernel': 'fp8_gemm_1d2d_kernel' if args.workload != 'fp8fp4' else 'fp8_fp4_gemm_kernel',
+                'frac': round(achieved / peak, 4), 'traffic': traffic,
+                'per': f'one step = {len(launches)} launch(es), one per shape; achieved = algorithmic '
+                       f'{"FLOPs" if bound == "mfma" else "bytes"} of the step / sum of per-launch durations; '
+                       f'traffic = calibrated HBM bytes (FETCH_SIZE + WRITE_SIZE) of the step',
+                'traffic_source': traffic_note,
+                'kernel': sorted({c.split(' kind=')[0] for c in configs}),
+                'launch_config': {l.name: c for l, c in zip(launches, configs)},
+                'algorithmic_bytes': {l.name: l.nbytes for l in launches},
                 'per_launch_us': {l.name: round(u, 2) for l, u in zip(launches, per)},
                 'per_launch_tflops': {l.name: round(l.flops / u / 1e6, 1) for l, u in zip(launches, per)},
                 'per_launch_gbs': {l.name: round(l.nbytes / u / 1e3, 1) for l, u in zip(launches, per)}}

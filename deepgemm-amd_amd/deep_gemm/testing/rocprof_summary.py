@@ -1,0 +1,209 @@
+"""Summaries of rocprofv3 CSV output for the bench workloads.
+
+Two inputs are understood:
+  * `<prefix>_kernel_trace.csv` of `rocprofv3 --kernel-trace --output-format csv`
+    (one row per dispatch, start/end timestamps in ns);
+  * `<prefix>_counter_collection.csv` of `rocprofv3 --pmc <COUNTER> --output-format csv`
+    (one row per dispatch and counter).
+
+GEMM dispatches are mapped to bench.py's launch names by dispatch order: bench.py
+runs `warmup` steps of all launches, then `max(5, steps)` back-to-back repetitions
+of each launch in turn (the per-launch timing phase), then `steps` timed steps.
+Only the per-launch phase is summarised, so each figure belongs to one shape.
+
+HBM traffic: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what the
+same counter reads for a plain copy kernel of known size (bench.py
+--calibrate-copy-mib launches torch.neg over that many MiB of float32: the
+kernel reads and writes exactly that many bytes), so a factor of 1.0 means the
+counter is exact.
+
+Usage:
+  python -m deep_gemm.testing.rocprof_summary \
+      --bench-json OUT/bench.json --trace OUT/k/x_kernel_trace.csv \
+      [--fetch OUT/f/x_counter_collection.csv --write OUT/w/x_counter_collection.csv \
+       --copy-mib 1024] [--warmup W --steps S] --md profiles/NAME.md [--json profiles/NAME.json]
+"""
+import argparse
+import csv
+import json
+import os
+import sys
+
+GEMM_KEYS = ('fp8_gemm_1d2d', 'fp8_fp4_gemm', 'fp8_gemm_1d2d_pipe')
+COPY_KEY = 'neg_kernel'
+
+
+def _is_gemm(name: str) -> bool:
+    return any(k in name for k in GEMM_KEYS)
+
+
+def _short(name: str) -> str:
+    """Kernel symbol without the argument list."""
+    name = name.replace('(anonymous namespace)::', '').replace('void ', '')
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == '<':
+            depth += 1
+        elif ch == '>':
+            depth -= 1
+        elif ch == '(' and depth == 0:
+            return name[:i]
+    return name
+
+
+def phase_slices(num_launches: int, warmup: int, steps: int):
+    """Index ranges, within the GEMM dispatch sequence, of each launch's
+    per-launch timing repetitions."""
+    reps = max(5, steps)
+    base = warmup * num_launches
+    return [range(base + i * reps, base + (i + 1) * reps) for i in range(num_launches)], reps
+
+
+def read_trace(path):
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r['Dispatch_Id']))
+    return rows
+
+
+def read_counters(path, counter):
+    """Dispatch_Id -> (kernel name, value) for one counter."""
+    out = {}
+    for r in csv.DictReader(open(path)):
+        if r['Counter_Name'] != counter:
+            continue
+        did = int(r['Dispatch_Id'])
+        name, val = r['Kernel_Name'], float(r['Counter_Value'])
+        prev = out.get(did)
+        out[did] = (name, val + (prev[1] if prev else 0.0))
+    return dict(sorted(out.items()))
+
+
+def gemm_sequence(items):
+    """GEMM entries of (dispatch_id, name, payload) in dispatch order."""
+    return [it for it in items if _is_gemm(it[1])]
+
+
+def summarize(args):
+    bench = json.loads(open(args.bench_json).read().strip().splitlines()[-1])
+    roof = bench['roofline']
+    names = list(roof['per_launch_us'].keys())
+    warmup = args.warmup if args.warmup is not None else bench['warmup']
+    steps = args.steps if args.steps is not None else bench['steps']
+    slices, reps = phase_slices(len(names), warmup, steps)
+
+    trace = read_trace(args.trace)
+    seq = gemm_sequence([(int(r['Dispatch_Id']), r['Kernel_Name'], r) for r in trace])
+    expected = (warmup + steps) * len(names) + reps * len(names)
+    if len(seq) != expected:
+        sys.exit(f'expected {expected} GEMM dispatches (warmup {warmup}, steps {steps}, '
+                 f'{len(names)} launches), found {len(seq)}')
+    per = []
+    for name, sl in zip(names, slices):
+        rows = [seq[i][2] for i in sl]
+        kern = {_short(r['Kernel_Name']) for r in rows}
+        durs = [(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3 for r in rows]
+        r0 = rows[0]
+        per.append({'launch': name, 'kernel': ' / '.join(sorted(kern)), 'calls': len(rows),
+                    'avg_us': sum(durs) / len(durs), 'min_us': min(durs), 'max_us': max(durs),
+                    'event_us': roof['per_launch_us'][name],
+                    'grid': int(r0['Grid_Size_X']) // max(1, int(r0['Workgroup_Size_X'])),
+                    'vgpr': int(r0['VGPR_Count']), 'agpr': int(r0['Accum_VGPR_Count']),
+                    'lds': int(r0['LDS_Block_Size'])})
+
+    traffic = None
+    if args.fetch and args.write:
+        traffic = {}
+        calib = {}
+        for counter, path in (('FETCH_SIZE', args.fetch), ('WRITE_SIZE', args.write)):
+            vals = read_counters(path, counter)
+            copies = [v for _, (n, v) in vals.items() if COPY_KEY in n]
+            if not copies:
+                sys.exit(f'{path}: no {COPY_KEY} dispatch (run bench.py with --calibrate-copy-mib)')
+            known_kib = args.copy_mib * 1024.0
+            factor = (sum(copies) / len(copies)) / known_kib
+            calib[counter] = {'copy_kib_read': sum(copies) / len(copies), 'copy_kib_known': known_kib,
+                              'factor': factor}
+            gseq = gemm_sequence([(d, n, v) for d, (n, v) in vals.items()])
+            # Under --pmc bench.py runs with the warmup/steps given on the command line.
+            psl, _ = phase_slices(len(names), args.pmc_warmup, args.pmc_steps)
+            exp = (args.pmc_warmup + args.pmc_steps) * len(names) + max(5, args.pmc_steps) * len(names)
+            if len(gseq) != exp:
+                sys.exit(f'{path}: expected {exp} GEMM dispatches, found {len(gseq)}')
+            for name, sl in zip(names, psl):
+                kib = sum(gseq[i][2] for i in sl) / len(sl)
+                traffic.setdefault(name, {})[counter] = kib * 1024.0 / factor
+        traffic = {'per_launch_bytes': {n: {'fetch': round(t['FETCH_SIZE']), 'write': round(t['WRITE_SIZE']),
+                                            'total': round(t['FETCH_SIZE'] + t['WRITE_SIZE'])}
+                                        for n, t in traffic.items()},
+                   'calibration': calib}
+
+    lines = []
+    lines.append(f"# {bench['config']['workload']}\n")
+    lines.append('Kernel durations from `rocprofv3 --kernel-trace --stats`, per-launch timing phase of '
+                 'bench.py (back-to-back repetitions of one shape), next to the HIP-event average that '
+                 'bench.py measured in the same run.\n')
+    lines.append('Commands (repository root on the GPU box; `OUT` = an output folder):\n')
+    lines.append('```')
+    for c in args.command or []:
+        lines.append(c)
+    lines.append('```\n')
+    lines.append('| launch | kernel | grid | VGPR/AGPR | LDS B | calls | rocprof avg us | min | max | '
+                 'bench event us |')
+    lines.append('|---|---|---|---|---|---|---|---|---|---|')
+    for p in per:
+        lines.append(f"| {p['launch']} | `{p['kernel']}` | {p['grid']} | {p['vgpr']}/{p['agpr']} | {p['lds']} | "
+                     f"{p['calls']} | {p['avg_us']:.1f} | {p['min_us']:.1f} | {p['max_us']:.1f} | "
+                     f"{p['event_us']:.1f} |")
+    lines.append('')
+    tot_r = sum(p['avg_us'] for p in per)
+    tot_e = sum(p['event_us'] for p in per)
+    lines.append(f'Sum over launches: rocprof {tot_r:.1f} us, bench events {tot_e:.1f} us '
+                 f'(ratio {tot_e / tot_r:.3f}).\n')
+    lines.append(f"bench.py line: value {bench['value']} {bench['unit']}, roofline achieved "
+                 f"{roof['achieved']} {roof['unit']} of {roof['peak']} (frac {roof['frac']}).\n")
+    if traffic:
+        lines.append('## HBM traffic (FETCH_SIZE / WRITE_SIZE, calibrated)\n')
+        for c, v in traffic['calibration'].items():
+            lines.append(f"- {c}: copy kernel read {v['copy_kib_read']:.0f} KiB for "
+                         f"{v['copy_kib_known']:.0f} KiB moved, factor {v['factor']:.4f}")
+        lines.append('')
+        lines.append('| launch | fetch MB | write MB | total MB | algorithmic MB | total / algorithmic |')
+        lines.append('|---|---|---|---|---|---|')
+        algo = roof.get('algorithmic_bytes', {})
+        for n, t in traffic['per_launch_bytes'].items():
+            a = algo.get(n)
+            ratio = f'{t["total"] / a:.2f}' if a else '-'
+            lines.append(f"| {n} | {t['fetch'] / 1e6:.1f} | {t['write'] / 1e6:.1f} | {t['total'] / 1e6:.1f} | "
+                         f"{(a or 0) / 1e6:.1f} | {ratio} |")
+        lines.append('')
+    os.makedirs(os.path.dirname(os.path.abspath(args.md)), exist_ok=True)
+    open(args.md, 'w').write('\n'.join(lines))
+    if args.json:
+        out = {'workload': bench['config']['workload'],
+               'launch_config': roof.get('launch_config', {}),
+               'kernel_us': {p['launch']: round(p['avg_us'], 2) for p in per}}
+        if traffic:
+            out.update(traffic)
+        open(args.json, 'w').write(json.dumps(out, indent=1) + '\n')
+    print('\n'.join(lines))
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--bench-json', required=True)
+    ap.add_argument('--trace', required=True)
+    ap.add_argument('--fetch')
+    ap.add_argument('--write')
+    ap.add_argument('--copy-mib', type=float, default=1024)
+    ap.add_argument('--warmup', type=int)
+    ap.add_argument('--steps', type=int)
+    ap.add_argument('--pmc-warmup', type=int, default=0)
+    ap.add_argument('--pmc-steps', type=int, default=1)
+    ap.add_argument('--md', required=True)
+    ap.add_argument('--json')
+    ap.add_argument('--command', action='append', help='command line to record in the summary')
+    summarize(ap.parse_args(argv))
+
+
+if __name__ == '__main__':
+    main()
