@@ -1,6 +1,6 @@
 """Benchmark of the FP8 block-scaled GEMM hot path on one MI355X.
 
-Default workload: dense fp8_gemm_nt at M = 4096 over
+Default workload (the headline configuration): dense fp8_gemm_nt at M = 4096 over
 the DeepSeek-V3 (N, K) sweep {(2112,7168), (24576,1536), (7168,16384),
 (4096,7168), (7168,2048)}, e4m3 operands with 1x128 / 128x128 FP32 scales, BF16
 output. One step = one call per shape (5 launches). `value` is total
@@ -257,24 +257,30 @@ def main():
             l.fn()
     torch.cuda.synchronize()
 
-    # Per-launch durations, HIP events on the launch stream (torch's current stream,
-    # which the library launches on), back-to-back repetitions of each launch.
+    # Per-launch durations: HIP events on the launch stream (torch's current stream,
+    # which the library launches on) around each repetition, with L2 and the 256 MB
+    # Infinity Cache flushed before it by zeroing a 512 MiB buffer, as the
+    # reference's bench_kineto flushes L2 (deep_gemm/testing/bench.py:76-104), so
+    # operands come from HBM.
     stream = torch.cuda.current_stream()
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device='cuda:0')
     per, configs = [], []
     for l in launches:
         reps = max(5, args.steps)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in evs:
+            flush.zero_()
+            e0.record(stream)
             l.fn()
-        e1.record(stream)
+            e1.record(stream)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
+        us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / reps
         per.append(us)
         configs.append(deep_gemm.get_last_config())
         log(f'  {l.name}: {us:8.1f} us  {l.flops / us / 1e6:7.1f} TFLOPS  {l.nbytes / us / 1e3:7.1f} GB/s  '
             f'[{deep_gemm.get_last_config()}]')
 
+    del flush
     # Whole-job timed region: K steps, synchronized on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
