@@ -251,6 +251,15 @@ const char* kind_name(GemmKind k) {
 // rounds of resident workgroups it needs times the work of one tile divided by
 // that candidate's relative throughput (measured MFMA efficiency of the tile
 // shape and pipeline). Grouped kinds need block_m to divide the row alignment.
+// Whether a block_m fits the contiguous / psum segment alignment: a block may
+// not straddle two groups, except that the pipelined kernel's 256-row tile runs
+// once per 128-row block when their experts differ (contiguous layout only).
+bool grouped_tile_ok(GemmKind kind, int variant, int bm, int align_m) {
+    if (kind == kContiguous) return align_m % bm == 0 || (variant == 2 && bm == 256 && align_m % 128 == 0);
+    if (kind == kPsum) return align_m % bm == 0;
+    return true;
+}
+
 TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k, int64_t groups, int align_m) {
     const int tv = g_tile_variant.load(), tm = g_tile_m.load(), tn = g_tile_n.load();
     // The pipelined kernel keeps one SFB value per K block in LDS (up to 1024 blocks).
@@ -258,22 +267,22 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     if (tv > 0) {
         const bool ok = tv == 1 ? fp8_1d2d_tile_supported(tm, tn) : (pipe_ok && fp8_1d2d_v2_tile_supported(tm, tn));
         if (!ok) DG_UNSUPPORTED("tile override not compiled");
-        if ((kind == kContiguous || kind == kPsum) && align_m % tm != 0)
-            DG_UNSUPPORTED("tile override block_m must divide the M alignment");
+        if (!grouped_tile_ok(kind, tv, tm, align_m))
+            DG_UNSUPPORTED("tile override block_m does not fit the M alignment");
         return {tm, tn, tv};
     }
     struct Cand { int variant, bm, bn, per_cu; double eff; };
     // Relative per-CU throughput of each kernel/tile, measured on MI355X at
     // M = 4096 over the DeepSeek-V3 shapes (pipelined 256 x 128 = 1.0).
     static const Cand cands[] = {
-        {2, 256, 128, 1, 1.00}, {2, 128, 256, 1, 0.97}, {2, 128, 128, 1, 0.80},
+        {2, 256, 256, 1, 1.32}, {2, 256, 128, 1, 1.00}, {2, 128, 256, 1, 0.97}, {2, 128, 128, 1, 0.80},
         {1, 128, 128, 2, 0.80}, {1, 128, 64, 3, 0.55}, {1, 64, 128, 3, 0.55}, {1, 64, 64, 4, 0.45}};
     int cus = 256;
     try { cus = num_sms_now(); } catch (const Error&) {}
     double best = 1e300;
     TileConfig out{64, 64, 1};
     for (const auto& c : cands) {
-        if ((kind == kContiguous || kind == kPsum) && align_m % c.bm != 0) continue;
+        if (!grouped_tile_ok(kind, c.variant, c.bm, align_m)) continue;
         if (c.variant == 2 && !pipe_ok) continue;
         const int64_t tiles = ceil_div(m_rows, c.bm) * ceil_div(n, c.bn) * groups;
         const int64_t slots = (int64_t)cus * c.per_cu;
@@ -355,7 +364,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
         const int64_t m_rows = m;
         const TileConfig t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
-        if ((kind == kContiguous || kind == kPsum) && align_m % t.block_m != 0)
+        if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
         if (t.variant == 2)

@@ -88,57 +88,96 @@ __device__ __forceinline__ void dma4_vaddr(const void* src, uint32_t lds) {
 }
 
 template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C>
-__global__ void __launch_bounds__(kThreads, 1)
-fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int num_n_blocks) {
-    static_assert(WGM * WGN == 4, "4 waves");
+__global__ void __launch_bounds__(WGM * WGN * 64, 1)
+fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int num_n_blocks, const int raster_gm) {
+    constexpr int NW = WGM * WGN;              // waves per workgroup (4: one per SIMD, 8: two per SIMD)
+    constexpr int NT = NW * 64;
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int SM = WM / 32, SN = WN / 32;
-    constexpr int A_INSTR = BM / 32;          // 1 KB wave loads per stage for A (4 waves x A_INSTR x 1 KB)
-    constexpr int B_INSTR = BN / 32;
+    constexpr int A_INSTR = BM / (8 * NW);     // 1 KB (8-row) wave loads per stage for A
+    constexpr int B_INSTR = BN / (8 * NW);
+    static_assert(A_INSTR * 8 * NW == BM && B_INSTR * 8 * NW == BN, "tile rows per wave load");
     constexpr int LOADS_PER_STAGE = A_INSTR + B_INSTR + 1;   // + one SFA load
     constexpr int SA_OFF = (BM + BN) * kBK;
-    constexpr int SA_ROWS_PER_WAVE = BM / 4;  // SFA rows loaded by each wave (<= 64)
-    constexpr int STAGE_BYTES = SA_OFF + 4 * 256;
+    constexpr int SA_ROWS_PER_WAVE = BM / NW;  // SFA rows loaded by each wave (<= 64)
+    constexpr int STAGE_BYTES = SA_OFF + NW * 256;
     static_assert(WN <= 128 && 128 % WN == 0, "a wave's N range must sit in one 128-row SFB block");
     static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
-    static_assert((STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
+    static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
     __shared__ float s_sfb[2][kMaxKBlocks];   // SFB of the block's (at most two) 128-row N groups
     __shared__ int s_flag;
+    __shared__ int s_half_valid[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
 
-    const Tile t = decode_tile<BM, BN, KIND>(p.m, p.n, p.num_groups, p.layout, p.align_m, p.zero_padding,
-                                             num_m_blocks, num_n_blocks, static_cast<uint16_t*>(p.d), p.ldd,
-                                             &s_flag);
+    const Tile t = decode_tile<BM, BN, KIND, NT>(p.m, p.n, p.num_groups, p.layout, p.align_m, p.zero_padding,
+                                                 num_m_blocks, num_n_blocks, static_cast<uint16_t*>(p.d), p.ldd,
+                                                 &s_flag, raster_gm);
     if (!t.active) return;
     const int m0 = t.m0, n0 = t.n0;
 
+    // A contiguous-layout tile of 256 rows covers two 128-row blocks (the host
+    // only runs it with a 128-multiple M alignment), and the expert of a block is
+    // max(0, grouped_layout[first row]). When both blocks hold rows to store and
+    // their experts differ, the tile runs one pass per block: pass q uses block
+    // q's expert, only the waves of rows [128q, 128q + 128) compute, and only
+    // those rows are stored.
+    int npass = 1;
+    int pass_expert[2] = {t.expert, t.expert};
+    if constexpr (KIND == kContiguous && BM > 128) {
+        static_assert(BM == 256 && WM == 128, "two 128-row blocks, one per wave row");
+        if (tid < 2) s_half_valid[tid] = 0;
+        __syncthreads();
+        for (int r = tid; r < BM; r += NT)
+            if (m0 + r < p.m && p.layout[m0 + r] >= 0) s_half_valid[r >> 7] = 1;
+        __syncthreads();
+        const int e_lo = min(max(0, p.layout[m0]), p.num_groups - 1);
+        const int e_hi = (m0 + 128 < p.m) ? min(max(0, p.layout[m0 + 128]), p.num_groups - 1) : e_lo;
+        if (!s_half_valid[1] || e_hi == e_lo) {
+            pass_expert[0] = e_lo;
+        } else if (!s_half_valid[0]) {
+            pass_expert[0] = e_hi;
+        } else {
+            npass = 2;
+            pass_expert[0] = e_lo;
+            pass_expert[1] = e_hi;
+        }
+    }
+
     const uint8_t* __restrict__ a_base =
         p.a + ((KIND == kMasked) ? (int64_t)t.g * p.a_gs : 0) + (int64_t)m0 * p.lda;
-    const uint8_t* __restrict__ b_base = p.b + (int64_t)t.expert * p.b_gs + (int64_t)n0 * p.ldb;
     const float* __restrict__ sa_base =
         p.sfa + ((KIND == kMasked) ? (int64_t)t.g * p.sfa_gs : 0) + (int64_t)m0 * p.sfa_sm;
 
     const int a_rows = min(BM, t.row_end - m0);
     const int b_rows = min(BN, p.n - n0);
     const int num_kb = (p.k + kBK - 1) / kBK;
+    const int my_group = (wn * WN) >> 7;
 
+    // One pass of the tile: the whole K loop and the epilogue. Written as a lambda
+    // called once (twice only for split contiguous tiles), since a loop around
+    // it costs registers even when it runs once.
+    auto run_pass = [&](const int pass) {
+    const int expert = pass_expert[pass];
+    const bool wave_computes = npass == 1 || wm == pass;
+    const uint8_t* __restrict__ b_base = p.b + (int64_t)expert * p.b_gs + (int64_t)n0 * p.ldb;
+    if (pass > 0) __syncthreads();   // every wave is done with the stage ring and s_sfb of the previous pass
     {
-        const float* sfb_g = p.sfb + (int64_t)t.expert * p.sfb_gs;
+        const float* sfb_g = p.sfb + (int64_t)expert * p.sfb_gs;
         const int last_row = (p.n - 1) >> 7;
-        for (int idx = tid; idx < 2 * num_kb; idx += kThreads) {
+        for (int idx = tid; idx < 2 * num_kb; idx += NT) {
             const int gsel = idx / num_kb, kb = idx % num_kb;
             const int row = min((n0 >> 7) + gsel, last_row);
             s_sfb[gsel][kb] = sfb_g[(int64_t)row * p.sfb_sn + (int64_t)kb * p.sfb_sk];
         }
     }
     __syncthreads();   // s_sfb visible; no stage loads are in flight yet
-    const int my_group = (wn * WN) >> 7;
 
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
@@ -204,7 +243,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
     auto mainloop = [&](auto bounds_tag) {
         constexpr bool BOUNDS = decltype(bounds_tag)::value;
         // Interior: one per-lane offset per operand. Segment s covers rows 8s..8s+7 and
-        // s = i*4 + wave, so the swizzle phase (bit 3 of the row) is wave & 1 for all s.
+        // s = i*NW + wave (NW even), so the swizzle phase (bit 3 of the row) is wave & 1.
         const uint32_t voff_a = rs * (uint32_t)p.lda + ((pc ^ swz_g((wave & 1) * 8 + rs)) << 4);
         const uint32_t voff_b = rs * (uint32_t)p.ldb + ((pc ^ swz_g((wave & 1) * 8 + rs)) << 4);
         const int sa_row = wave * SA_ROWS_PER_WAVE + lane;
@@ -218,12 +257,12 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
                 const uint8_t* b_kb = b_base + kb * kBK;
 #pragma unroll
                 for (int i = 0; i < A_INSTR; ++i) {
-                    const int seg = i * 4 + wave;
+                    const int seg = i * NW + wave;
                     dma16_saddr(a_kb + (int64_t)seg * 8 * p.lda, voff_a, stage_lds + seg * 1024);
                 }
 #pragma unroll
                 for (int i = 0; i < B_INSTR; ++i) {
-                    const int seg = i * 4 + wave;
+                    const int seg = i * NW + wave;
                     dma16_saddr(b_kb + (int64_t)seg * 8 * p.ldb, voff_b, stage_lds + BM * kBK + seg * 1024);
                 }
                 dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
@@ -231,7 +270,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
             } else {
 #pragma unroll
                 for (int i = 0; i < A_INSTR; ++i) {
-                    const int seg = i * 4 + wave;
+                    const int seg = i * NW + wave;
                     const int r = seg * 8 + rs;
                     const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
                     const void* src = (r < a_rows && k < p.k) ? (const void*)(a_base + (int64_t)r * p.lda + k)
@@ -240,7 +279,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
                 }
 #pragma unroll
                 for (int i = 0; i < B_INSTR; ++i) {
-                    const int seg = i * 4 + wave;
+                    const int seg = i * NW + wave;
                     const int r = seg * 8 + rs;
                     const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
                     const void* src = (r < b_rows && k < p.k) ? (const void*)(b_base + (int64_t)r * p.ldb + k)
@@ -265,7 +304,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
             else
                 wait_vmcnt_barrier<0>();
             if (kb + STAGES - 1 < num_kb) issue_stage(kb + STAGES - 1, (kb + STAGES - 1) % STAGES);
-            compute(kb);
+            if (wave_computes) compute(kb);
         }
     };
 
@@ -283,6 +322,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
         const int m = m0 + wm * WM + i * 32 + lrow;
         bool store, zero;
         row_predicate<KIND>(t, p.m, p.layout, m, store, zero);
+        if (npass == 2 && ((m - m0) >> 7) != pass) store = false;
         if (!store && !zero) continue;
 #pragma unroll
         for (int j = 0; j < SN; ++j) {
@@ -295,8 +335,31 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
                                        zero ? 0.f : f[q * 4 + 0], zero ? 0.f : f[q * 4 + 1],
                                        zero ? 0.f : f[q * 4 + 2], zero ? 0.f : f[q * 4 + 3]);
             }
+            // Keep C reads next to their stores: hoisting every sub-tile's C
+            // loads above the stores would hold them all in registers at once.
+            asm volatile("" ::: "memory");
         }
     }
+    };   // run_pass
+
+    run_pass(0);
+    if constexpr (KIND == kContiguous && BM > 128) {
+        if (npass == 2) run_pass(1);
+    }
+}
+
+// Band height (in m blocks) of the tile raster: the 32 workgroups an XCD runs
+// at once then read about gm A panels and 32 / gm B panels per K block; pick
+// the gm that minimizes those bytes.
+inline int choose_raster_gm(int bm, int bn, int num_m_blocks) {
+    int best = 1;
+    double best_bytes = 1e30;
+    for (int gm = 1; gm <= 32; gm *= 2) {
+        if (gm > num_m_blocks) break;
+        const double bytes = (double)gm * bm + (32.0 / gm) * bn;
+        if (bytes < best_bytes) best_bytes = bytes, best = gm;
+    }
+    return best;
 }
 
 template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND>
@@ -308,10 +371,11 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     if (grid == 0) return;
     DG_CHECK(grid < (int64_t)1 << 31);
     DG_CHECK((a.k + kBK - 1) / kBK <= kMaxKBlocks);
-    const dim3 gdim(static_cast<unsigned>(grid)), bdim(kThreads);
+    const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
+    const dim3 gdim(static_cast<unsigned>(grid)), bdim(WGM * WGN * 64);
 #define DG_PIPE_LAUNCH(OF, HC)                                                                                   \
     hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC>), gdim, bdim, 0, stream, \
-                       a, num_m_blocks, num_n_blocks)
+                       a, num_m_blocks, num_n_blocks, raster_gm)
     if constexpr (KIND != kNormal) {
         DG_CHECK(!a.out_f32 && a.c == nullptr);
         DG_PIPE_LAUNCH(0, 0);
@@ -338,12 +402,14 @@ void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
 }  // namespace
 
 bool fp8_1d2d_v2_tile_supported(int bm, int bn) {
-    return (bm == 256 && bn == 128) || (bm == 128 && bn == 256) || (bm == 128 && bn == 128);
+    return (bm == 256 && bn == 256) || (bm == 256 && bn == 128) || (bm == 128 && bn == 256) ||
+           (bm == 128 && bn == 128);
 }
 
 void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args, hipStream_t stream) {
     const int key = cfg.block_m * 1000 + cfg.block_n;
     switch (key) {
+        case 256256: launch_tile<256, 256, 2, 4, 2>(kind, args, stream); break;   // 8 waves of 128 x 64
         case 256128: launch_tile<256, 128, 2, 2, 3>(kind, args, stream); break;   // waves 128 x 64
         case 128256: launch_tile<128, 256, 1, 4, 3>(kind, args, stream); break;   // waves 128 x 64
         case 128128: launch_tile<128, 128, 2, 2, 4>(kind, args, stream); break;   // waves 64 x 64

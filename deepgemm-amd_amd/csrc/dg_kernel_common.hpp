@@ -37,12 +37,13 @@ __device__ __forceinline__ uint16_t bf16_bits(float x) { return __builtin_bit_ca
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-// Workgroups are handed to the 8 XCDs round-robin; give each XCD a contiguous
-// range of logical tiles so neighbouring tiles (which share A rows or B
-// columns) meet in the same L2.
+// Workgroups are handed to the 8 XCDs round-robin (workgroup b runs on XCD
+// b % 8); give each XCD a contiguous range of logical tiles so neighbouring
+// tiles (which share A rows or B columns) meet in the same L2. XCD x holds
+// grid / 8 workgroups, plus one when x < grid % 8; the map is a bijection.
 __device__ __forceinline__ int xcd_remap(int bid, int grid) {
-    if ((grid & 7) != 0) return bid;
-    return (bid & 7) * (grid >> 3) + (bid >> 3);
+    const int q = grid >> 3, r = grid & 7, x = bid & 7;
+    return x * q + min(x, r) + (bid >> 3);
 }
 
 // Byte offset of 16-byte chunk `c` of row `r` in an LDS tile whose rows are
@@ -68,11 +69,30 @@ struct Tile {
     int active;    // 0: nothing to compute (the block may still have been zero-filled)
 };
 
+// Tile index -> (m block, n block) in bands of `raster_gm` m-blocks: inside a
+// band, m varies fastest, so a run of consecutive tiles covers a raster_gm x
+// (run / raster_gm) patch and reads raster_gm A panels and run / raster_gm B
+// panels. raster_gm <= 0 or >= num_m_blocks gives plain column order.
+__device__ __forceinline__ void raster_tile(int tile, int num_m_blocks, int num_n_blocks, int raster_gm, int& mb,
+                                            int& nb) {
+    if (raster_gm <= 0 || raster_gm >= num_m_blocks) {
+        mb = tile % num_m_blocks;
+        nb = tile / num_m_blocks;
+        return;
+    }
+    const int band = tile / (raster_gm * num_n_blocks);
+    const int r = tile - band * raster_gm * num_n_blocks;
+    const int gm = min(raster_gm, num_m_blocks - band * raster_gm);
+    mb = band * raster_gm + r % gm;
+    nb = r / gm;
+}
+
 // `layout` is m_indices (contiguous), masked_m (masked) or psum ends (psum).
-template <int BM, int BN, int KIND>
+// NT = threads per workgroup.
+template <int BM, int BN, int KIND, int NT = kThreads>
 __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const int32_t* __restrict__ layout,
                                             int align_m, int zero_padding, int num_m_blocks, int num_n_blocks,
-                                            uint16_t* zero_d, int64_t ldd, int* s_flag) {
+                                            uint16_t* zero_d, int64_t ldd, int* s_flag, int raster_gm = 0) {
     Tile t{};
     int tile = xcd_remap(blockIdx.x, gridDim.x);
     if constexpr (KIND == kMasked) {
@@ -80,8 +100,10 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
         t.g = tile / per_group;
         tile -= t.g * per_group;
     }
-    t.m0 = (tile % num_m_blocks) * BM;
-    t.n0 = (tile / num_m_blocks) * BN;
+    int mb, nb;
+    raster_tile(tile, num_m_blocks, num_n_blocks, raster_gm, mb, nb);
+    t.m0 = mb * BM;
+    t.n0 = nb * BN;
     t.row_end = m;
     t.active = 1;
     if constexpr (KIND == kMasked) {
@@ -95,7 +117,8 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
         t.expert = min(max(0, layout[t.m0]), num_groups - 1);
         if (threadIdx.x == 0) *s_flag = 0;
         __syncthreads();
-        if (threadIdx.x < BM && t.m0 + (int)threadIdx.x < m && layout[t.m0 + threadIdx.x] >= 0) *s_flag = 1;
+        for (int r = threadIdx.x; r < BM; r += NT)
+            if (t.m0 + r < m && layout[t.m0 + r] >= 0) *s_flag = 1;
         __syncthreads();
         t.active = *s_flag;
     } else if constexpr (KIND == kPsum) {
@@ -122,7 +145,7 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
             t.active = 0;
             if (zero_padding) {
                 const int r_hi = min(t.m0 + BM, aend);
-                for (int idx = threadIdx.x; idx < (r_hi - t.m0) * BN; idx += kThreads) {
+                for (int idx = threadIdx.x; idx < (r_hi - t.m0) * BN; idx += NT) {
                     const int r = t.m0 + idx / BN, c = t.n0 + idx % BN;
                     if (c < n) zero_d[(int64_t)r * ldd + c] = 0;
                 }
@@ -181,9 +204,17 @@ __device__ __forceinline__ void store4(void* __restrict__ d, const void* __restr
         uint16_t* dp = static_cast<uint16_t*>(d) + d_off;
         if constexpr (HAS_C) {
             const uint16_t* cp = static_cast<const uint16_t*>(c) + c_off;
+            if (full) {
+                const uint2 cv = *reinterpret_cast<const uint2*>(cp);
+                v[0] = bf16_to_f32(static_cast<uint16_t>(cv.x & 0xffffu)) + v[0];
+                v[1] = bf16_to_f32(static_cast<uint16_t>(cv.x >> 16)) + v[1];
+                v[2] = bf16_to_f32(static_cast<uint16_t>(cv.y & 0xffffu)) + v[2];
+                v[3] = bf16_to_f32(static_cast<uint16_t>(cv.y >> 16)) + v[3];
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (n + e < n_total) v[e] = bf16_to_f32(cp[e]) + v[e];
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < n_total) v[e] = bf16_to_f32(cp[e]) + v[e];
+            }
         }
         if (full) {
             *reinterpret_cast<uint2*>(dp) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};

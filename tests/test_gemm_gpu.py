@@ -77,15 +77,16 @@ def test_dense_bf16_vs_oracle(m, n, k):
         assert ogemm.calc_diff(out, raw) < 1e-3
 
 
-def test_all_tiles_bitwise_equal():
-    """Every compiled tile shape gives the same bits (each output's K order is fixed)."""
-    m, n, k = 200, 320, 1024
+@pytest.mark.parametrize('m,n,k', [(200, 320, 1024), (512, 768, 2048), (300, 520, 1040)])
+def test_all_tiles_bitwise_equal(m, n, k):
+    """Every compiled tile shape gives the same bits (each output's K order is fixed).
+    (512, 768, 2048) has interior tiles for every shape; the others are ragged."""
     x = gen.dense_inputs(m, n, k, seed=5)
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
     outs = []
     try:
         for v, bm, bn in ((1, 64, 64), (1, 64, 128), (1, 128, 64), (1, 128, 128),
-                          (2, 128, 128), (2, 128, 256), (2, 256, 128)):
+                          (2, 128, 128), (2, 128, 256), (2, 256, 128), (2, 256, 256)):
             deep_gemm.set_tile_override(bm, bn, variant=v)
             d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
             deep_gemm.fp8_gemm_nt(a, b, d)
@@ -183,10 +184,29 @@ def test_k_zero_and_empty():
 
 # ----------------------------------------------------------------- grouped
 
-def test_contiguous_vs_oracle_and_dense():
-    ms, aligned = gen.contiguous_sizes(4, 900, seed=7)
+CONTIG_TILES = [None, (2, 256, 256), (2, 128, 256), (1, 128, 128)]
+
+
+@pytest.mark.parametrize('tile', CONTIG_TILES)
+@pytest.mark.parametrize('ms', [None, [130, 100, 300, 0, 250, 1]])
+def test_contiguous_vs_oracle_and_dense(tile, ms):
+    """Random segments, and segments whose 128-aligned boundaries fall inside
+    256-row tiles (a tile then holds two experts)."""
+    if ms is None:
+        ms, aligned = gen.contiguous_sizes(4, 900, seed=7)
+    else:
+        aligned = [(mi + 127) // 128 * 128 for mi in ms]
     n, k = 384, 1024
-    print(f'contiguous ms={ms} aligned={aligned}', flush=True)
+    print(f'contiguous ms={ms} aligned={aligned} tile={tile}', flush=True)
+    if tile is not None:
+        deep_gemm.set_tile_override(tile[1], tile[2], variant=tile[0])
+    try:
+        _contiguous_case(ms, aligned, n, k)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+
+
+def _contiguous_case(ms, aligned, n, k):
     x = gen.contiguous_inputs(ms, aligned, n, k, seed=7)
     a_deq = oquant.dequant_per_token(x['qa'], x['sfa'])
     b_deq = np.stack([oquant.dequant_per_block(x['qb'][i], x['sfb'][i]) for i in range(len(ms))])
