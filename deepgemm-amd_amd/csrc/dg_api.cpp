@@ -335,6 +335,9 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
     const bool grouped_a = kind == kMasked;
 
     if (is_1d2d(o, r)) {
+        // The kernels move K in 16-byte chunks; a partial chunk would pull in the
+        // bytes past K of a padded row.
+        if (k % 16 != 0) DG_UNSUPPORTED("K must be a multiple of 16 on the FP32-scale FP8 path");
         check_vector_alignment(o.a, "a");
         check_vector_alignment(o.b, "b");
         check_vector_alignment(o.d, "d");

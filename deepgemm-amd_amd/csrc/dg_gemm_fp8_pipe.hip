@@ -53,10 +53,12 @@ __device__ __attribute__((aligned(16))) uint8_t g_zero_page[16] = {0};
 __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 __device__ __forceinline__ int swz16(int r, int c) { return r * 128 + ((c ^ swz_g(r)) << 4); }
 
+// Wait until at most N of this wave's vector loads are in flight and its LDS
+// reads have returned, then barrier.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_barrier() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // LDS byte address of a pointer into __shared__ memory.
@@ -87,7 +89,8 @@ __device__ __forceinline__ void dma4_vaddr(const void* src, uint32_t lds) {
                  : "memory", "m0");
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C>
+// KT: K is not a multiple of 128 (the last K block is partial).
+template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT>
 __global__ void __launch_bounds__(WGM * WGN * 64, 1)
 fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int num_n_blocks, const int raster_gm) {
     constexpr int NW = WGM * WGN;              // waves per workgroup (4: one per SIMD, 8: two per SIMD)
@@ -165,7 +168,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
     // it costs registers even when it runs once.
     auto run_pass = [&](const int pass) {
     const int expert = pass_expert[pass];
-    const bool wave_computes = npass == 1 || wm == pass;
+    // (`p.m >= 0` always holds. Keeping the condition a run-time value stops the
+    // compiler from moving promotion code across the stage barrier, which pushed
+    // register use past the 256 a wave has at two waves per SIMD.)
+    const bool wave_computes = (npass == 1 || wm == pass) && p.m >= 0;
     const uint8_t* __restrict__ b_base = p.b + (int64_t)expert * p.b_gs + (int64_t)n0 * p.ldb;
     if (pass > 0) __syncthreads();   // every wave is done with the stage ring and s_sfb of the previous pass
     {
@@ -191,128 +197,271 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
 #pragma unroll
             for (int e = 0; e < 16; ++e) fin[i][j][e] = 0.f;
 
-    // 32 consecutive K bytes (chunks c, c+1) of row r of an LDS tile.
-    auto frag = [&](const uint8_t* tile, int r, int c) {
-        const i32x4 lo = *reinterpret_cast<const i32x4*>(tile + swz16(r, c));
-        const i32x4 hi = *reinterpret_cast<const i32x4*>(tile + swz16(r, c + 1));
+    // MFMA fragment of a 32-row slab: lane (lrow, lhalf) takes row r0 + lrow,
+    // chunks c and c + 1 with c = 4 * ks + 2 * lhalf (K bytes [64ks + 32lhalf, +32)).
+    // Slab first rows r0 are multiples of 32, so the swizzle phase of the lane's
+    // row, and with it the lane's byte offset inside the slab, is the same for
+    // every slab: four per-lane offsets serve all fragment reads.
+    const int gl = swz_g(lrow);
+    uint32_t frag_off[2][2];   // [ks][lo/hi chunk]
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) frag_off[ks][h] = lrow * 128 + (((4 * ks + 2 * lhalf + h) ^ gl) << 4);
+    auto frag = [&](const uint8_t* tile, int r0, int ks) {
+        const uint8_t* slab = tile + r0 * 128;
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(slab + frag_off[ks][0]);
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(slab + frag_off[ks][1]);
         return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
-    auto compute = [&](int kb) {
+    // ---- global -> LDS stage loads
+    // Fast path (K a multiple of 128): one wave-uniform SGPR base per operand and
+    // K block plus a per-lane 32-bit offset. Rows past the tile's valid rows are
+    // clamped to the last valid row: they load a copy of it, and the outputs they
+    // feed (M or N positions past the edge) are never stored.
+    // K-tail path (KT): lanes whose row or K chunk is out of range read a zero page.
+    // Segment s (8 rows) of a stage is loaded by wave s % NW; since NW is even the
+    // swizzle phase of its rows, and so the lane's chunk, is the same for all of a
+    // wave's segments. Each load's per-lane offset (row clamped, chunk) is
+    // computed at issue time, without branches: `launder` keeps the compiler from
+    // hoisting the offsets into registers held across the loop, and a branch in
+    // the middle of the MFMA sequence would cost registers too.
+    const uint32_t chunk_off = (pc ^ swz_g((wave & 1) * 8 + rs)) << 4;
+    const int sa_row = wave * SA_ROWS_PER_WAVE + lane;
+    const uint32_t voff_sa = (uint32_t)(min(sa_row, a_rows - 1) * p.sfa_sm) * 4u;
+    auto launder = [](int v) {
+        asm volatile("" : "+v"(v));
+        return v;
+    };
+    auto clamped_voff = [&](int seg, int rows, int ld) {
+        const int r = min(seg * 8 + launder(rs), rows - 1);
+        return (uint32_t)r * (uint32_t)ld + chunk_off;
+    };
+
+    const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    auto issue_stage = [&](int kb, int st) {
+        const uint32_t stage_lds = smem_lds + st * STAGE_BYTES;
+        if constexpr (!KT) {
+            const uint8_t* a_kb = a_base + (int64_t)kb * kBK;
+            const uint8_t* b_kb = b_base + (int64_t)kb * kBK;
+#pragma unroll
+            for (int i = 0; i < A_INSTR; ++i) {
+                const int seg = i * NW + wave;
+                dma16_saddr(a_kb, clamped_voff(seg, a_rows, p.lda), stage_lds + seg * 1024);
+            }
+#pragma unroll
+            for (int i = 0; i < B_INSTR; ++i) {
+                const int seg = i * NW + wave;
+                dma16_saddr(b_kb, clamped_voff(seg, b_rows, p.ldb), stage_lds + BM * kBK + seg * 1024);
+            }
+            dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
+                       stage_lds + SA_OFF + wave * 256);
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_INSTR; ++i) {
+                const int seg = i * NW + wave;
+                const int r = seg * 8 + launder(rs);
+                const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
+                const void* src = (r < a_rows && k < p.k) ? (const void*)(a_base + (int64_t)r * p.lda + k)
+                                                          : (const void*)g_zero_page;
+                dma16_vaddr(src, stage_lds + seg * 1024);
+            }
+#pragma unroll
+            for (int i = 0; i < B_INSTR; ++i) {
+                const int seg = i * NW + wave;
+                const int r = seg * 8 + launder(rs);
+                const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
+                const void* src = (r < b_rows && k < p.k) ? (const void*)(b_base + (int64_t)r * p.ldb + k)
+                                                          : (const void*)g_zero_page;
+                dma16_vaddr(src, stage_lds + BM * kBK + seg * 1024);
+            }
+            const void* src = (lane < SA_ROWS_PER_WAVE && sa_row < a_rows)
+                                  ? (const void*)(sa_base + (int64_t)sa_row * p.sfa_sm + (int64_t)kb * p.sfa_sk)
+                                  : (const void*)g_zero_page;
+            dma4_vaddr(src, stage_lds + SA_OFF + wave * 256);
+        }
+    };
+
+    // ---- fragments and scales of a stage
+    // opB: the wave's B fragments of the whole K block; opA: A fragments of one
+    // 32-row slice, double-buffered so slice i + 1 is read while slice i computes.
+    i32x8 opB[SN][2], opA[2][2];
+    float sa_cur[SM];
+    // sa * sb of the lane's rows for K block kb (read at the top of the block's
+    // compute; the stage slot is refilled only after the next barrier).
+    auto load_scales = [&](int kb) {
         const uint8_t* sbase = smem + (kb % STAGES) * STAGE_BYTES;
-        const uint8_t* a_tile = sbase;
-        const uint8_t* b_tile = sbase + BM * kBK;
         const float sb = s_sfb[my_group][kb];
-        float sa[SM];
 #pragma unroll
         for (int i = 0; i < SM; ++i) {
             const int r = wm * WM + i * 32 + lrow;
-            sa[i] = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
-                                                    (r % SA_ROWS_PER_WAVE) * 4) * sb;
+            sa_cur[i] = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
+                                                        (r % SA_ROWS_PER_WAVE) * 4) * sb;
         }
-        i32x8 op_n[SN][2];
+    };
+    auto load_stage_frags = [&](int kb) {
+        const uint8_t* sbase = smem + (kb % STAGES) * STAGE_BYTES;
 #pragma unroll
         for (int j = 0; j < SN; ++j)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) op_n[j][ks] = frag(b_tile, wn * WN + j * 32 + lrow, ks * 4 + lhalf * 2);
-
-        // Tiles in order t = i * SN + j; acc[t & 1] holds tile t while tile t - 1 is promoted.
-        f32x16 acc[2];
-        i32x8 om0 = frag(a_tile, wm * WM + lrow, lhalf * 2);
-        i32x8 om1 = frag(a_tile, wm * WM + lrow, 4 + lhalf * 2);
-#pragma unroll
-        for (int tt = 0; tt <= SM * SN; ++tt) {
-            if (tt < SM * SN) {
-                const int i = tt / SN, j = tt % SN;
-                if (j == 0 && i > 0) {
-                    om0 = frag(a_tile, wm * WM + i * 32 + lrow, lhalf * 2);
-                    om1 = frag(a_tile, wm * WM + i * 32 + lrow, 4 + lhalf * 2);
-                }
-                f32x16 c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op_n[j][0], om0, f32x16{}, 0, 0, 0, 0, 0,
-                                                                           0);
-                acc[tt & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(op_n[j][1], om1, c, 0, 0, 0, 0, 0, 0);
-            }
-            if (tt > 0) {
-                const int pt = tt - 1, i = pt / SN, j = pt % SN;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) fin[i][j][e] = __builtin_fmaf(sa[i], acc[pt & 1][e], fin[i][j][e]);
-            }
-        }
+            for (int ks = 0; ks < 2; ++ks)
+                opB[j][ks] = frag(sbase + BM * kBK, wn * WN + j * 32, ks);
+        opA[0][0] = frag(sbase, wm * WM, 0);
+        opA[0][1] = frag(sbase, wm * WM, 1);
     };
 
-    auto mainloop = [&](auto bounds_tag) {
-        constexpr bool BOUNDS = decltype(bounds_tag)::value;
-        // Interior: one per-lane offset per operand. Segment s covers rows 8s..8s+7 and
-        // s = i*NW + wave (NW even), so the swizzle phase (bit 3 of the row) is wave & 1.
-        const uint32_t voff_a = rs * (uint32_t)p.lda + ((pc ^ swz_g((wave & 1) * 8 + rs)) << 4);
-        const uint32_t voff_b = rs * (uint32_t)p.ldb + ((pc ^ swz_g((wave & 1) * 8 + rs)) << 4);
-        const int sa_row = wave * SA_ROWS_PER_WAVE + lane;
-        const uint32_t voff_sa = lane < SA_ROWS_PER_WAVE ? (uint32_t)(sa_row * p.sfa_sm) * 4u : 0u;
-
-        const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
-        auto issue_stage = [&](int kb, int st) {
-            const uint32_t stage_lds = smem_lds + st * STAGE_BYTES;
-            if constexpr (!BOUNDS) {
-                const uint8_t* a_kb = a_base + kb * kBK;
-                const uint8_t* b_kb = b_base + kb * kBK;
-#pragma unroll
-                for (int i = 0; i < A_INSTR; ++i) {
-                    const int seg = i * NW + wave;
-                    dma16_saddr(a_kb + (int64_t)seg * 8 * p.lda, voff_a, stage_lds + seg * 1024);
-                }
-#pragma unroll
-                for (int i = 0; i < B_INSTR; ++i) {
-                    const int seg = i * NW + wave;
-                    dma16_saddr(b_kb + (int64_t)seg * 8 * p.ldb, voff_b, stage_lds + BM * kBK + seg * 1024);
-                }
-                dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
-                           stage_lds + SA_OFF + wave * 256);
-            } else {
-#pragma unroll
-                for (int i = 0; i < A_INSTR; ++i) {
-                    const int seg = i * NW + wave;
-                    const int r = seg * 8 + rs;
-                    const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
-                    const void* src = (r < a_rows && k < p.k) ? (const void*)(a_base + (int64_t)r * p.lda + k)
-                                                              : (const void*)g_zero_page;
-                    dma16_vaddr(src, stage_lds + seg * 1024);
-                }
-#pragma unroll
-                for (int i = 0; i < B_INSTR; ++i) {
-                    const int seg = i * NW + wave;
-                    const int r = seg * 8 + rs;
-                    const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
-                    const void* src = (r < b_rows && k < p.k) ? (const void*)(b_base + (int64_t)r * p.ldb + k)
-                                                              : (const void*)g_zero_page;
-                    dma16_vaddr(src, stage_lds + BM * kBK + seg * 1024);
-                }
-                const void* src = (lane < SA_ROWS_PER_WAVE && sa_row < a_rows)
-                                      ? (const void*)(sa_base + (int64_t)sa_row * p.sfa_sm + (int64_t)kb * p.sfa_sk)
-                                      : (const void*)g_zero_page;
-                dma4_vaddr(src, stage_lds + SA_OFF + wave * 256);
-            }
-        };
-
-#pragma unroll
-        for (int s = 0; s < STAGES - 1; ++s)
-            if (s < num_kb) issue_stage(s, s);
-
-        for (int kb = 0; kb < num_kb; ++kb) {
-            // Loads for kb are complete once at most (STAGES - 2) later stages remain in flight.
-            if (kb + STAGES - 2 < num_kb)
+    // Loads for stage s are complete once at most the stages issued after it
+    // remain in flight (vector loads retire in order).
+    // (With two stages the count is always 0; a branch here would split the
+    // unrolled MFMA sequence and wreck register allocation.)
+    auto wait_stage = [&](int s) {
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (STAGES == 2) {
+            wait_vmcnt_barrier<0>();
+        } else {
+            if (s + STAGES - 2 < num_kb)
                 wait_vmcnt_barrier<(STAGES - 2) * LOADS_PER_STAGE>();
             else
                 wait_vmcnt_barrier<0>();
-            if (kb + STAGES - 1 < num_kb) issue_stage(kb + STAGES - 1, (kb + STAGES - 1) % STAGES);
-            if (wave_computes) compute(kb);
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
-    const bool interior = a_rows == BM && b_rows == BN && (p.k % kBK) == 0;
-    if (interior)
-        mainloop(std::false_type{});
+    if constexpr (!KT) {
+    // Prologue: every slot is free, so the first STAGES stages are issued at once.
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s)
+        if (s < num_kb) issue_stage(s, s);
+    __builtin_amdgcn_sched_barrier(0);
+    if (num_kb >= STAGES)
+        wait_vmcnt_barrier<(STAGES - 1) * LOADS_PER_STAGE>();
     else
-        mainloop(std::true_type{});
+        wait_vmcnt_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave_computes) load_stage_frags(0);
+
+    // Sub-tiles t = i * SN + j in order; acc[j] holds sub-tile (i, j). After the
+    // MFMA pair of sub-tile t is issued, sub-tile t - 1 is promoted, so the FMAs
+    // run while the matrix core works.
+    // The stage hand-off (wait for stage kb + 1, barrier) sits before the last
+    // 32-row slice of K block kb: every read of stage kb has been issued (slice
+    // SM - 1's A fragment was read one slice ahead) and has returned (the wait
+    // includes lgkmcnt), so the barrier also frees stage kb's slot, and stage
+    // kb + STAGES is loaded into it right away. The next block's A fragment is
+    // then read before, and each B fragment right after, the last MFMAs that use
+    // the registers, so their LDS latency hides under those MFMAs.
+    static_assert(SM % 2 == 0, "A fragment double buffer: the next block's first slice goes to buffer 0");
+    f32x16 acc[SN];
+    for (int kb = 0; kb < num_kb; ++kb) {
+        if (!wave_computes) {
+            wait_stage(kb + 1);
+            issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES);
+        } else {
+        load_scales(kb);
+        const uint8_t* a_tile = smem + (kb % STAGES) * STAGE_BYTES;
+        const uint8_t* next = smem + ((kb + 1) % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+            const int cur = i & 1;
+            if (i + 1 < SM) {
+                opA[cur ^ 1][0] = frag(a_tile, wm * WM + (i + 1) * 32, 0);
+                opA[cur ^ 1][1] = frag(a_tile, wm * WM + (i + 1) * 32, 1);
+            } else {
+                // (unconditional: in the last block this reads a stale slot, unused)
+                wait_stage(kb + 1);
+                // (the index is clamped rather than branched on: a branch here costs
+                // registers. Past the last block this re-loads the last stage into the
+                // free slot; nothing reads it.)
+                issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES);
+                opA[0][0] = frag(next, wm * WM, 0);
+                opA[0][1] = frag(next, wm * WM, 1);
+            }
+#pragma unroll
+            for (int j = 0; j < SN; ++j) {
+                const f32x16 c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(opB[j][0], opA[cur][0], f32x16{}, 0,
+                                                                                 0, 0, 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(opB[j][1], opA[cur][1], c, 0, 0, 0, 0, 0,
+                                                                         0);
+                if (i + 1 == SM) {
+                    // keep the reload after the MFMAs that read the old registers
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        opB[j][ks] = frag(next + BM * kBK, wn * WN + j * 32, ks);
+                }
+                // promote the previous sub-tile
+                const int pj = j > 0 ? j - 1 : SN - 1;
+                const int pi = j > 0 ? i : i - 1;
+                if (pi >= 0) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) fin[pi][pj][e] = __builtin_fmaf(sa_cur[pi], acc[pj][e], fin[pi][pj][e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            fin[SM - 1][SN - 1][e] = __builtin_fmaf(sa_cur[SM - 1], acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
+        }
+    }
+
+    } else {
+        // K tail: a simpler schedule. The stage loads use per-lane 64-bit
+        // addresses with a zero page for out-of-range chunks, too many live
+        // values to sit inside the MFMA sequence, so the hand-off is at the top of
+        // each block: wait for stage kb (which also certifies that every wave is
+        // done with stage kb - 1), refill that slot, then compute kb.
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s)
+            if (s < num_kb) issue_stage(s, s);
+        f32x16 acc[SN];
+        for (int kb = 0; kb < num_kb; ++kb) {
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (STAGES == 2) {
+                wait_vmcnt_barrier<0>();
+            } else {
+                if (kb + STAGES - 2 < num_kb)
+                    wait_vmcnt_barrier<(STAGES - 2) * LOADS_PER_STAGE>();
+                else
+                    wait_vmcnt_barrier<0>();
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (kb + STAGES - 1 < num_kb) issue_stage(kb + STAGES - 1, (kb + STAGES - 1) % STAGES);
+            if (wave_computes) {
+                load_scales(kb);
+                load_stage_frags(kb);
+                const uint8_t* a_tile = smem + (kb % STAGES) * STAGE_BYTES;
+#pragma unroll
+                for (int i = 0; i < SM; ++i) {
+                    const int cur = i & 1;
+                    if (i + 1 < SM) {
+                        opA[cur ^ 1][0] = frag(a_tile, wm * WM + (i + 1) * 32, 0);
+                        opA[cur ^ 1][1] = frag(a_tile, wm * WM + (i + 1) * 32, 1);
+                    }
+#pragma unroll
+                    for (int j = 0; j < SN; ++j) {
+                        const f32x16 c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                            opB[j][0], opA[cur][0], f32x16{}, 0, 0, 0, 0, 0, 0);
+                        acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(opB[j][1], opA[cur][1], c, 0, 0,
+                                                                                 0, 0, 0, 0);
+                        const int pj = j > 0 ? j - 1 : SN - 1;
+                        const int pi = j > 0 ? i : i - 1;
+                        if (pi >= 0) {
+#pragma unroll
+                            for (int e = 0; e < 16; ++e)
+                                fin[pi][pj][e] = __builtin_fmaf(sa_cur[pi], acc[pj][e], fin[pi][pj][e]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    fin[SM - 1][SN - 1][e] =
+                        __builtin_fmaf(sa_cur[SM - 1], acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
+            }
+        }
+    }
+    // No stage load may still be writing LDS when the workgroup ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // Epilogue: lane owns column m of each 32x32 tile; registers 4q..4q+3 are
     // rows n = 8q + 4*lhalf + 0..3 of that tile.
@@ -373,9 +522,16 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     DG_CHECK((a.k + kBK - 1) / kBK <= kMaxKBlocks);
     const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
     const dim3 gdim(static_cast<unsigned>(grid)), bdim(WGM * WGN * 64);
-#define DG_PIPE_LAUNCH(OF, HC)                                                                                   \
-    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC>), gdim, bdim, 0, stream, \
-                       a, num_m_blocks, num_n_blocks, raster_gm)
+    const bool k_tail = (a.k % kBK) != 0;
+#define DG_PIPE_LAUNCH(OF, HC)                                                                                       \
+    do {                                                                                                             \
+        if (k_tail)                                                                                                  \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 1>), gdim, bdim, 0, \
+                               stream, a, num_m_blocks, num_n_blocks, raster_gm);                                   \
+        else                                                                                                         \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0>), gdim, bdim, 0, \
+                               stream, a, num_m_blocks, num_n_blocks, raster_gm);                                   \
+    } while (0)
     if constexpr (KIND != kNormal) {
         DG_CHECK(!a.out_f32 && a.c == nullptr);
         DG_PIPE_LAUNCH(0, 0);
