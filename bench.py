@@ -178,6 +178,11 @@ def make_fp8fp4():
     a = deep_gemm.per_token_cast_to_fp8(torch.randn((m, k), generator=gen).bfloat16().to(dev), use_ue8m0=True)
     b = deep_gemm.per_token_cast_to_fp4(torch.randn((n, k), generator=gen).bfloat16().to(dev), use_ue8m0=True,
                                         gran_k=32)
+    # Scales in the kernel's packed MN-major UE8M0 form, transformed once up front
+    # as for weights (the reference transforms FP32 SFs inside each call and times
+    # the GEMM kernel alone, tests/test_fp8_fp4.py:84-86,100).
+    a = (a[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(a[1]))
+    b = (b[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(b[1]))
     d = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
     fn = (lambda: deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, 128), recipe_b=(1, 32)))
     nbytes = m * k + n * k // 2 + 4 * m * (k // 128) + 4 * n * (k // 32) + 2 * m * n

@@ -252,8 +252,8 @@ const char* kind_name(GemmKind k) {
 // that candidate's relative throughput (measured MFMA efficiency of the tile
 // shape and pipeline). Grouped kinds need block_m to divide the row alignment.
 // Whether a block_m fits the contiguous / psum segment alignment: a block may
-// not straddle two groups, except that the pipelined kernel's 256-row tile runs
-// once per 128-row block when their experts differ (contiguous layout only).
+// not straddle two groups, except that the LDS-pipelined kernels' 256-row tile
+// runs once per 128-row block when their experts differ (contiguous layout only).
 bool grouped_tile_ok(GemmKind kind, int variant, int bm, int align_m) {
     if (kind == kContiguous) return align_m % bm == 0 || (variant == 2 && bm == 256 && align_m % 128 == 0);
     if (kind == kPsum) return align_m % bm == 0;
@@ -415,6 +415,18 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
         args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
         args.sfb_row_shift = r.gran_mn_b == 128 ? 7 : 0;
+        // The 256 x 256 pipelined kernel takes packed scale words and K % 128 == 0;
+        // everything else runs on the 128 x 128 kernel. A tile override selects
+        // the kernel by its variant (1: 128 x 128, 2: pipelined).
+        const int tv = g_tile_variant.load();
+        const bool pipe_ok = fp8_fp4_pipe_supported(args) && grouped_tile_ok(kind, 2, 256, align_m);
+        if (tv == 2 && !pipe_ok) DG_UNSUPPORTED("tile override: the pipelined UE8M0 kernel does not take these inputs");
+        if (pipe_ok && tv != 1) {
+            const TileConfig t{256, 256, 2};
+            record_config("fp8_fp4_gemm_ue8m0_pipe", kind, t, m, n, k, groups);
+            launch_fp8_fp4_gemm_pipe(kind, args, stream);
+            return;
+        }
         const TileConfig t{128, 128, 1};
         if ((kind == kContiguous || kind == kPsum) && align_m % t.block_m != 0)
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 128 on the UE8M0 path");

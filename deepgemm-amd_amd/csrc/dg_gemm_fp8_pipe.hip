@@ -38,6 +38,7 @@
 
 #include "dg_internal.hpp"
 #include "dg_kernel_common.hpp"
+#include "dg_lds_dma.hpp"
 
 namespace dgm {
 namespace {
@@ -47,47 +48,7 @@ using namespace dev;
 constexpr int kBK = 128;
 constexpr int kMaxKBlocks = 1024;   // K up to 131072 on this path (the host routes longer K elsewhere)
 
-// Source for lanes whose row or K chunk is out of range.
-__device__ __attribute__((aligned(16))) uint8_t g_zero_page[16] = {0};
-
 __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
-__device__ __forceinline__ int swz16(int r, int c) { return r * 128 + ((c ^ swz_g(r)) << 4); }
-
-// Wait until at most N of this wave's vector loads are in flight and its LDS
-// reads have returned, then barrier.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_barrier() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-
-// LDS byte address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_address(const uint8_t* p) {
-    return static_cast<uint32_t>(reinterpret_cast<size_t>((const __attribute__((address_space(3))) uint8_t*)p));
-}
-
-// Direct global -> LDS loads, written as inline asm so that the compiler does
-// not track them: its LDS-DMA alias analysis cannot tell the ring's stages
-// apart and would drain every in-flight stage before each LDS read. The kernel
-// orders them itself with s_waitcnt vmcnt + s_barrier. Each wave instruction
-// writes lds + lane * size; M0 holds the wave-uniform LDS base (M0 is not
-// otherwise live in these kernels).
-__device__ __forceinline__ void dma16_saddr(const uint8_t* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma4_saddr(const uint8_t* base, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_vaddr(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma4_vaddr(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src)
-                 : "memory", "m0");
-}
 
 // KT: K is not a multiple of 128 (the last K block is partial).
 template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT>
@@ -168,10 +129,17 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
     // it costs registers even when it runs once.
     auto run_pass = [&](const int pass) {
     const int expert = pass_expert[pass];
-    // (`p.m >= 0` always holds. Keeping the condition a run-time value stops the
-    // compiler from moving promotion code across the stage barrier, which pushed
-    // register use past the 256 a wave has at two waves per SIMD.)
-    const bool wave_computes = (npass == 1 || wm == pass) && p.m >= 0;
+    // In a masked group with few rows, a wave whose rows all lie past them only
+    // loads and synchronizes. (`p.m >= 0` always holds; keeping the condition a
+    // run-time value stops the compiler from moving promotion code across the
+    // stage barrier, which pushed register use past the 256 a wave has at two
+    // waves per SIMD. readfirstlane: the value is wave-uniform and the compiler
+    // must see it so, or code merged below the branch gets per-lane LDS addresses.)
+    bool wave_computes;
+    if constexpr (KIND == kMasked)
+        wave_computes = __builtin_amdgcn_readfirstlane((int)(wm * WM < a_rows && p.m >= 0)) != 0;
+    else
+        wave_computes = (npass == 1 || wm == pass) && p.m >= 0;
     const uint8_t* __restrict__ b_base = p.b + (int64_t)expert * p.b_gs + (int64_t)n0 * p.ldb;
     if (pass > 0) __syncthreads();   // every wave is done with the stage ring and s_sfb of the previous pass
     {
@@ -230,10 +198,6 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
     const uint32_t chunk_off = (pc ^ swz_g((wave & 1) * 8 + rs)) << 4;
     const int sa_row = wave * SA_ROWS_PER_WAVE + lane;
     const uint32_t voff_sa = (uint32_t)(min(sa_row, a_rows - 1) * p.sfa_sm) * 4u;
-    auto launder = [](int v) {
-        asm volatile("" : "+v"(v));
-        return v;
-    };
     auto clamped_voff = [&](int seg, int rows, int ld) {
         const int r = min(seg * 8 + launder(rs), rows - 1);
         return (uint32_t)r * (uint32_t)ld + chunk_off;
@@ -567,7 +531,7 @@ void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8Gemm
     switch (key) {
         case 256256: launch_tile<256, 256, 2, 4, 2>(kind, args, stream); break;   // 8 waves of 128 x 64
         case 256128: launch_tile<256, 128, 2, 2, 3>(kind, args, stream); break;   // waves 128 x 64
-        case 128256: launch_tile<128, 256, 1, 4, 3>(kind, args, stream); break;   // waves 128 x 64
+        case 128256: launch_tile<128, 256, 2, 4, 3>(kind, args, stream); break;   // 8 waves of 64 x 64
         case 128128: launch_tile<128, 128, 2, 2, 4>(kind, args, stream); break;   // waves 64 x 64
         default: DG_UNSUPPORTED("tile shape not compiled for the pipelined FP32-scale FP8 kernel");
     }

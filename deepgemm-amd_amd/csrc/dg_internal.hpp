@@ -80,7 +80,7 @@ struct Fp8GemmArgs {
 struct TileConfig {
     int block_m;
     int block_n;
-    int variant = 1;   // FP32-scale kernels: 1 = register-staged 32x32x64, 2 = LDS-pipelined 16x16x128
+    int variant = 1;   // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined
 };
 
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
@@ -123,6 +123,10 @@ struct Fp8Fp4GemmArgs {
 
 void launch_fp8_fp4_gemm(GemmKind kind, const TileConfig& cfg, const Fp8Fp4GemmArgs& args,
                          hipStream_t stream);
+// 256 x 256 LDS-pipelined UE8M0 kernel: packed MN-major scale words of both
+// operands (SFB one row per N row) and K a multiple of 128.
+bool fp8_fp4_pipe_supported(const Fp8Fp4GemmArgs& args);
+void launch_fp8_fp4_gemm_pipe(GemmKind kind, const Fp8Fp4GemmArgs& args, hipStream_t stream);
 
 // SF layout kernels.
 struct SfTransposeArgs {

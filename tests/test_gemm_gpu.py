@@ -363,6 +363,192 @@ def test_fp8_fp4_vs_oracle(m, n, k, a_fp4, gka):
     assert torch.equal(d.view(torch.int16), d2.view(torch.int16))
 
 
+# ------------------------------------------------- UE8M0: 256 x 256 pipelined kernel
+
+def _ue8m0_quant(x, fp4, gran):
+    """Codes and FP32 power-of-two SFs of one operand (rows x K), and its dequant."""
+    if fp4:
+        q, sf = oquant.per_token_cast_to_fp4(x, use_ue8m0=True, gran_k=gran)
+        return q, sf, oquant.dequant_fp4(q, sf, gran)
+    q, sf = oquant.per_token_cast_to_fp8(x, use_ue8m0=True, gran_k=gran)
+    return q, sf, oquant.dequant_per_token(q, sf, gran)
+
+
+def _ue8m0_grouped(x, fp4, gran):
+    """_ue8m0_quant over the leading group axis."""
+    parts = [_ue8m0_quant(x[i], fp4, gran) for i in range(x.shape[0])]
+    return tuple(np.stack([p[j] for p in parts]) for j in range(3))
+
+
+def _codes_dev(q, fp4):
+    return gen.to_dev(q, torch.int8) if fp4 else e4m3(q)
+
+
+def _packed(sf):
+    """FP32 power-of-two SFs -> packed MN-major UE8M0 words on the device."""
+    return deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(f32(sf))
+
+
+def _run_both_kernels(fn):
+    """Runs fn() on the 128 x 128 UE8M0 kernel and on the pipelined one; returns
+    (outputs, configs) of both."""
+    outs, cfgs = [], []
+    try:
+        for v, bm, bn in ((1, 128, 128), (2, 256, 256)):
+            deep_gemm.set_tile_override(bm, bn, variant=v)
+            outs.append(fn())
+            cfgs.append(deep_gemm.get_last_config())
+            print(cfgs[-1], flush=True)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    assert 'pipe' in cfgs[1] and 'pipe' not in cfgs[0]
+    return outs, cfgs
+
+
+UE8M0_DENSE = [
+    # m, n, k, a_fp4, b_fp4, gran_k_a, gran_k_b
+    (512, 768, 1024, False, True, 128, 32),    # config 5 recipe, interior tiles
+    (300, 520, 640, False, True, 128, 32),     # ragged M and N, 5 K blocks (gran-128 word tail)
+    (1, 64, 128, False, True, 128, 32),        # one row, one K block
+    (257, 384, 768, False, False, 32, 32),     # e4m3 x e4m3, 1x32 scales
+    (200, 256, 512, False, False, 128, 128),   # e4m3 x e4m3, 1x128 scales
+    (320, 448, 1024, True, True, 32, 32),      # e2m1 x e2m1
+    (130, 300, 384, True, False, 32, 128),     # e2m1 x e4m3
+]
+
+
+@pytest.mark.parametrize('m,n,k,a_fp4,b_fp4,gka,gkb', UE8M0_DENSE)
+def test_ue8m0_pipe_dense(m, n, k, a_fp4, b_fp4, gka, gkb):
+    """Pipelined UE8M0 kernel: oracle parity, the same bits as the 128 x 128 kernel
+    (same MFMA, same per-output K order), bounds and 20-rerun determinism."""
+    print(f'ue8m0 pipe dense m={m} n={n} k={k} a_fp4={a_fp4} b_fp4={b_fp4} gk=({gka},{gkb})', flush=True)
+    qa, sfa, a_deq = _ue8m0_quant(gen.randn_bf16((m, k), m + 3), a_fp4, gka)
+    qb, sfb, b_deq = _ue8m0_quant(gen.randn_bf16((n, k), n + 5), b_fp4, gkb)
+    ref = ogemm.gemm_nt(a_deq, b_deq)
+    a = (_codes_dev(qa, a_fp4), _packed(sfa))
+    b = (_codes_dev(qb, b_fp4), _packed(sfb))
+    # d is a strided view (row pitch a multiple of 16 bytes); the rest must stay untouched
+    big = sentinel_bf16((m + 8, (n + 72 + 7) // 8 * 8))
+
+    def call():
+        big.view(torch.int16).fill_(SENTINEL)
+        d = big[:m, :n]
+        deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, gka), recipe_b=(1, gkb))
+        torch.cuda.synchronize()
+        return big.clone()
+
+    (old, new), _ = _run_both_kernels(call)
+    out = new[:m, :n].float().cpu().numpy()
+    diff, _ = report('ue8m0 pipe', out, ref)
+    assert diff < 1e-5   # power-of-two scales: only FP32 accumulation and BF16 rounding remain
+    assert torch.equal(old.view(torch.int16), new.view(torch.int16))
+    outside = torch.ones_like(new, dtype=torch.bool)
+    outside[:m, :n] = False
+    assert bool((new.view(torch.int16)[outside] == SENTINEL).all())
+    # determinism (heuristic dispatch picks the pipelined kernel)
+    d = big[:m, :n]
+    for _ in range(20):
+        deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, gka), recipe_b=(1, gkb))
+    assert 'pipe' in deep_gemm.get_last_config()
+    assert torch.equal(big.view(torch.int16), new.view(torch.int16))
+
+
+@pytest.mark.parametrize('out_f32,with_c', [(True, True), (True, False), (False, True)])
+def test_ue8m0_pipe_dense_c_and_f32(out_f32, with_c):
+    m, n, k = 384, 512, 512
+    qa, sfa, a_deq = _ue8m0_quant(gen.randn_bf16((m, k), 61), False, 128)
+    qb, sfb, b_deq = _ue8m0_quant(gen.randn_bf16((n, k), 62), True, 32)
+    c_np = gen.randn_bf16((m, n), 63).astype(np.float32)
+    ref = ogemm.gemm_nt(a_deq, b_deq, c_np if with_c else None)
+    a = (e4m3(qa), _packed(sfa))
+    b = (gen.to_dev(qb, torch.int8), _packed(sfb))
+    dt = torch.float32 if out_f32 else torch.bfloat16
+    c = torch.from_numpy(c_np).to(dt).to(DEV) if with_c else None
+
+    def call():
+        d = torch.empty((m, n), dtype=dt, device=DEV)
+        deep_gemm.fp8_fp4_gemm_nt(a, b, d, c=c, recipe_a=(1, 128), recipe_b=(1, 32))
+        torch.cuda.synchronize()
+        return d
+
+    (old, new), _ = _run_both_kernels(call)
+    diff, _ = report(f'ue8m0 pipe f32={out_f32} c={with_c}', new.float().cpu().numpy(), ref)
+    assert diff < 1e-5
+    assert torch.equal(old, new)
+
+
+def test_ue8m0_pipe_masked():
+    g, max_m, n, k = 5, 320, 384, 768
+    masked = np.array([0, 1, 128, 320, 200], np.int32)
+    qa, sfa, a_deq = _ue8m0_grouped(gen.randn_bf16((g, max_m, k), 71), False, 128)
+    qb, sfb, b_deq = _ue8m0_grouped(gen.randn_bf16((g, n, k), 72), True, 32)
+    ref, valid = ogemm.gemm_masked(a_deq, b_deq, masked)
+    a = (e4m3(qa), _packed(sfa))
+    b = (gen.to_dev(qb, torch.int8), _packed(sfb))
+    mm = gen.to_dev(masked)
+
+    def call():
+        d = sentinel_bf16((g, max_m, n))
+        deep_gemm.m_grouped_fp8_fp4_gemm_nt_masked(a, b, d, mm, 128, recipe_a=(1, 128), recipe_b=(1, 32))
+        torch.cuda.synchronize()
+        return d
+
+    (old, new), _ = _run_both_kernels(call)
+    out = new.float().cpu().numpy()
+    diff, _ = report('ue8m0 pipe masked', out[valid], ref[valid])
+    assert diff < 1e-5
+    assert bool((new.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
+    assert torch.equal(old.view(torch.int16), new.view(torch.int16))
+    # each group equals the dense call on its valid rows
+    for i in range(g):
+        r = int(masked[i])
+        if r:
+            dd = torch.empty((r, n), dtype=torch.bfloat16, device=DEV)
+            deep_gemm.fp8_fp4_gemm_nt((a[0][i, :r], _packed(sfa[i, :r])), (b[0][i], b[1][i]), dd,
+                                      recipe_a=(1, 128), recipe_b=(1, 32))
+            assert torch.equal(dd.view(torch.int16), new[i, :r].view(torch.int16)), f'group {i}'
+
+
+@pytest.mark.parametrize('ms', [[130, 100, 300, 0, 250, 1], [256, 512, 128]])
+def test_ue8m0_pipe_contiguous(ms):
+    """Segments 128-aligned, so 256-row tiles straddle two experts (two-pass tiles)."""
+    aligned = [(mi + 127) // 128 * 128 for mi in ms]
+    g, n, k = len(ms), 384, 512
+    m_pad = sum(aligned)
+    m_indices = np.full(m_pad, -1, np.int32)
+    start = 0
+    for i, (mi, ai) in enumerate(zip(ms, aligned)):
+        m_indices[start:start + mi] = i
+        start += ai
+    qa, sfa, a_deq = _ue8m0_quant(gen.randn_bf16((m_pad, k), 81), False, 128)
+    qb, sfb, b_deq = _ue8m0_grouped(gen.randn_bf16((g, n, k), 82), True, 32)
+    ref, valid = ogemm.gemm_contiguous(a_deq, b_deq, m_indices)
+    a = (e4m3(qa), _packed(sfa))
+    b = (gen.to_dev(qb, torch.int8), _packed(sfb))
+    mi_dev = gen.to_dev(m_indices)
+
+    def call():
+        d = sentinel_bf16((m_pad, n))
+        deep_gemm.m_grouped_fp8_fp4_gemm_nt_contiguous(a, b, d, mi_dev, recipe_a=(1, 128), recipe_b=(1, 32))
+        torch.cuda.synchronize()
+        return d
+
+    (old, new), _ = _run_both_kernels(call)
+    out = new.float().cpu().numpy()
+    diff, _ = report('ue8m0 pipe contiguous', out[valid], ref[valid])
+    assert diff < 1e-5
+    assert bool((new.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
+    assert torch.equal(old.view(torch.int16), new.view(torch.int16))
+    start = 0
+    for i, (mi, ai) in enumerate(zip(ms, aligned)):
+        if mi:
+            dd = torch.empty((mi, n), dtype=torch.bfloat16, device=DEV)
+            deep_gemm.fp8_fp4_gemm_nt((a[0][start:start + mi], _packed(sfa[start:start + mi])), (b[0][i], b[1][i]),
+                                      dd, recipe_a=(1, 128), recipe_b=(1, 32))
+            assert torch.equal(dd.view(torch.int16), new[start:start + mi].view(torch.int16)), f'segment {i}'
+        start += ai
+
+
 # ----------------------------------------------------------------- quantizers
 
 def test_product_quantizers_match_oracle_on_gpu():
