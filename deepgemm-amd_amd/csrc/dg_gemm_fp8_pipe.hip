@@ -38,6 +38,7 @@
 
 #include "dg_internal.hpp"
 #include "dg_kernel_common.hpp"
+#include "dg_epilogue.hpp"
 #include "dg_lds_dma.hpp"
 
 namespace dgm {
@@ -424,34 +425,22 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
             }
         }
     }
-    // No stage load may still be writing LDS when the workgroup ends.
+    // No stage load may still be writing LDS when the workgroup ends (or the
+    // epilogue reuses it).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // Epilogue: lane owns column m of each 32x32 tile; registers 4q..4q+3 are
-    // rows n = 8q + 4*lhalf + 0..3 of that tile.
-    const int64_t d_goff = (KIND == kMasked) ? (int64_t)t.g * p.d_gs : 0;
-#pragma unroll
-    for (int i = 0; i < SM; ++i) {
-        const int m = m0 + wm * WM + i * 32 + lrow;
-        bool store, zero;
-        row_predicate<KIND>(t, p.m, p.layout, m, store, zero);
-        if (npass == 2 && ((m - m0) >> 7) != pass) store = false;
-        if (!store && !zero) continue;
-#pragma unroll
-        for (int j = 0; j < SN; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = n0 + wn * WN + j * 32 + q * 8 + lhalf * 4;
-                if (n >= p.n) continue;
-                const f32x16& f = fin[i][j];
-                store4<OUT_F32, HAS_C>(p.d, p.c, d_goff + (int64_t)m * p.ldd + n, (int64_t)m * p.ldc + n, n, p.n,
-                                       zero ? 0.f : f[q * 4 + 0], zero ? 0.f : f[q * 4 + 1],
-                                       zero ? 0.f : f[q * 4 + 2], zero ? 0.f : f[q * 4 + 3]);
-            }
-            // Keep C reads next to their stores: hoisting every sub-tile's C
-            // loads above the stores would hold them all in registers at once.
-            asm volatile("" ::: "memory");
-        }
+    // Epilogue through LDS (row-coalesced stores): every wave is done with the
+    // stage ring after this barrier; each then owns NW-th of the LDS.
+    __syncthreads();
+    {
+        using Epi = RowEpilogue<KIND, OUT_F32, HAS_C, SM, SN>;
+        constexpr int REGION = (STAGES * STAGE_BYTES / NW) / 16 * 16;
+        const int64_t d_goff = (KIND == kMasked) ? (int64_t)t.g * p.d_gs : 0;
+        const int m_lo = npass == 2 ? m0 + pass * 128 : m0;
+        const int m_hi = npass == 2 ? m_lo + 128 : m0 + BM;
+        Epi::template run<Epi::rows_per_pass(REGION)>(fin, smem + wave * REGION, lane, t, p.m, p.layout,
+                                                      m0 + wm * WM, n0 + wn * WN, p.n, m_lo, m_hi, p.d, p.c, p.ldd,
+                                                      p.ldc, d_goff);
     }
     };   // run_pass
 
