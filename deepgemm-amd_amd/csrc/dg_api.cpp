@@ -255,7 +255,7 @@ const char* kind_name(GemmKind k) {
 // not straddle two groups, except that the LDS-pipelined kernels' 256-row tile
 // runs once per 128-row block when their experts differ (contiguous layout only).
 bool grouped_tile_ok(GemmKind kind, int variant, int bm, int align_m) {
-    if (kind == kContiguous) return align_m % bm == 0 || (variant == 2 && bm == 256 && align_m % 128 == 0);
+    if (kind == kContiguous) return align_m % bm == 0 || (variant >= 2 && bm == 256 && align_m % 128 == 0);
     if (kind == kPsum) return align_m % bm == 0;
     return true;
 }
@@ -264,6 +264,11 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     const int tv = g_tile_variant.load(), tm = g_tile_m.load(), tn = g_tile_n.load();
     // The pipelined kernel keeps one SFB value per K block in LDS (up to 1024 blocks).
     const bool pipe_ok = ceil_div(k, 128) <= 1024;
+    if (tv == 4) {   // persistent form of the pipelined kernel
+        if (!pipe_ok || tm != 256 || tn != 256) DG_UNSUPPORTED("tile override: the persistent kernel is 256 x 256");
+        if (!grouped_tile_ok(kind, tv, tm, align_m)) DG_UNSUPPORTED("tile override block_m does not fit the M alignment");
+        return {256, 256, 4};
+    }
     if (tv > 0) {
         const bool ok = tv == 1 ? fp8_1d2d_tile_supported(tm, tn) : (pipe_ok && fp8_1d2d_v2_tile_supported(tm, tn));
         if (!ok) DG_UNSUPPORTED("tile override not compiled");
@@ -365,12 +370,14 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.sfa_gs = grouped_a ? o.sfa.stride(0) : 0;
         args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
         args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
+        args.grid_limit = 256;
+        try { args.grid_limit = num_sms_now(); } catch (const Error&) {}
         const int64_t m_rows = m;
         const TileConfig t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
         if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
-        if (t.variant == 2)
+        if (t.variant >= 2)
             launch_fp8_gemm_1d2d_v2(kind, t, args, stream);
         else
             launch_fp8_gemm_1d2d(kind, t, args, stream);
@@ -721,8 +728,9 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
             g_tile_variant = 0, g_tile_m = 0, g_tile_n = 0;
             return;
         }
-        const bool ok = variant == 1 ? fp8_1d2d_tile_supported(block_m, block_n)
-                                     : (variant == 2 && fp8_1d2d_v2_tile_supported(block_m, block_n));
+        const bool ok = variant == 1   ? fp8_1d2d_tile_supported(block_m, block_n)
+                        : variant == 2 ? fp8_1d2d_v2_tile_supported(block_m, block_n)
+                                       : (variant == 4 && block_m == 256 && block_n == 256);
         if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;
         g_tile_variant = variant;

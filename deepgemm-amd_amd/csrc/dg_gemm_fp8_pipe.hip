@@ -34,6 +34,7 @@
 //    accumulator column is one token row m (one sfa per lane).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "dg_internal.hpp"
@@ -52,9 +53,15 @@ constexpr int kMaxKBlocks = 1024;   // K up to 131072 on this path (the host rou
 __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
 // KT: K is not a multiple of 128 (the last K block is partial).
-template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT>
+// PERSIST: persistent workgroups (grid = CU count) walk the launch's tile
+// sequence with stride gridDim.x, the reference's scheduler
+// (scheduler/gemm.cuh:185-272, masked group walk :188-204, psum walk :205-225;
+// decode_tile_persistent). Otherwise one workgroup per tile and the hardware
+// dispatcher starts the next tile as a CU frees up.
+template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT, int PERSIST>
 __global__ void __launch_bounds__(WGM * WGN * 64, 1)
-fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int num_n_blocks, const int raster_gm) {
+fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const int num_n_blocks,
+                          const int raster_gm) {
     constexpr int NW = WGM * WGN;              // waves per workgroup (4: one per SIMD, 8: two per SIMD)
     constexpr int NT = NW * 64;
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
@@ -76,15 +83,31 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
     __shared__ int s_flag;
     __shared__ int s_half_valid[2];
 
-    const int tid = threadIdx.x;
+    const int slot = xcd_remap(blockIdx.x, gridDim.x);
+    for (int lt = slot;; lt += gridDim.x) {
+    // Persistent: per-tile copies of the arguments and the lane id, re-read each
+    // iteration so that nothing but the tile index is held across tiles (holding
+    // them costs registers in the K loop).
+    const Fp8GemmArgs p = PERSIST ? reload_kernel_args<Fp8GemmArgs>() : p_arg;
+    const int tid = PERSIST ? launder(threadIdx.x) : (int)threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
 
-    const Tile t = decode_tile<BM, BN, KIND, NT>(p.m, p.n, p.num_groups, p.layout, p.align_m, p.zero_padding,
-                                                 num_m_blocks, num_n_blocks, static_cast<uint16_t*>(p.d), p.ldd,
-                                                 &s_flag, raster_gm);
-    if (!t.active) return;
+    PTile t{};
+    if constexpr (PERSIST) {
+        if (lt != slot) __syncthreads();   // every wave is done with the previous tile's LDS
+        t = decode_tile_persistent<BM, BN, KIND, NT>(lt, p.m, p.n, p.num_groups, p.layout, p.align_m, p.zero_padding,
+                                                     num_m_blocks, num_n_blocks, static_cast<uint16_t*>(p.d), p.ldd,
+                                                     &s_flag, raster_gm);
+        if (t.done) break;
+        if (!t.active) continue;
+    } else {
+        static_cast<Tile&>(t) = decode_tile<BM, BN, KIND, NT>(p.m, p.n, p.num_groups, p.layout, p.align_m,
+                                                              p.zero_padding, num_m_blocks, num_n_blocks,
+                                                              static_cast<uint16_t*>(p.d), p.ldd, &s_flag, raster_gm);
+        if (!t.active) return;
+    }
     const int m0 = t.m0, n0 = t.n0;
 
     // A contiguous-layout tile of 256 rows covers two 128-row blocks (the host
@@ -448,6 +471,8 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p, const int num_m_blocks, const int
     if constexpr (KIND == kContiguous && BM > 128) {
         if (npass == 2) run_pass(1);
     }
+    if constexpr (!PERSIST) break;
+    }   // tile loop
 }
 
 // Band height (in m blocks) of the tile raster: the 32 workgroups an XCD runs
@@ -464,26 +489,27 @@ inline int choose_raster_gm(int bm, int bn, int num_m_blocks) {
     return best;
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND>
+template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int PERSIST>
 void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     const int num_n_blocks = (a.n + BN - 1) / BN;
     const int num_m_blocks = (a.m + BM - 1) / BM;
     int64_t grid = (int64_t)num_m_blocks * num_n_blocks;
-    if (KIND == kMasked) grid *= a.num_groups;
+    if (KIND == kMasked) grid *= a.num_groups;   // persistent: an upper bound (the kernel walks masked_m)
     if (grid == 0) return;
     DG_CHECK(grid < (int64_t)1 << 31);
     DG_CHECK((a.k + kBK - 1) / kBK <= kMaxKBlocks);
+    if (PERSIST) grid = std::min<int64_t>(grid, std::max(1, a.grid_limit));
     const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
     const dim3 gdim(static_cast<unsigned>(grid)), bdim(WGM * WGN * 64);
     const bool k_tail = (a.k % kBK) != 0;
 #define DG_PIPE_LAUNCH(OF, HC)                                                                                       \
     do {                                                                                                             \
         if (k_tail)                                                                                                  \
-            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 1>), gdim, bdim, 0, \
-                               stream, a, num_m_blocks, num_n_blocks, raster_gm);                                   \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 1, PERSIST>), gdim, \
+                               bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
         else                                                                                                         \
-            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0>), gdim, bdim, 0, \
-                               stream, a, num_m_blocks, num_n_blocks, raster_gm);                                   \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST>), gdim, \
+                               bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
     } while (0)
     if constexpr (KIND != kNormal) {
         DG_CHECK(!a.out_f32 && a.c == nullptr);
@@ -497,13 +523,13 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     DG_HIP_CHECK(hipGetLastError());
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES>
+template <int BM, int BN, int WGM, int WGN, int STAGES, int PERSIST = 0>
 void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
     switch (kind) {
-        case kNormal: launch_kind<BM, BN, WGM, WGN, STAGES, kNormal>(a, stream); break;
-        case kContiguous: launch_kind<BM, BN, WGM, WGN, STAGES, kContiguous>(a, stream); break;
-        case kMasked: launch_kind<BM, BN, WGM, WGN, STAGES, kMasked>(a, stream); break;
-        case kPsum: launch_kind<BM, BN, WGM, WGN, STAGES, kPsum>(a, stream); break;
+        case kNormal: launch_kind<BM, BN, WGM, WGN, STAGES, kNormal, PERSIST>(a, stream); break;
+        case kContiguous: launch_kind<BM, BN, WGM, WGN, STAGES, kContiguous, PERSIST>(a, stream); break;
+        case kMasked: launch_kind<BM, BN, WGM, WGN, STAGES, kMasked, PERSIST>(a, stream); break;
+        case kPsum: launch_kind<BM, BN, WGM, WGN, STAGES, kPsum, PERSIST>(a, stream); break;
         default: DG_UNSUPPORTED("unknown GEMM kind");
     }
 }
@@ -517,6 +543,11 @@ bool fp8_1d2d_v2_tile_supported(int bm, int bn) {
 
 void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args, hipStream_t stream) {
     const int key = cfg.block_m * 1000 + cfg.block_n;
+    if (cfg.variant == 4) {   // persistent workgroups
+        if (key != 256256) DG_UNSUPPORTED("the persistent pipelined kernel is compiled for 256 x 256 tiles only");
+        launch_tile<256, 256, 2, 4, 2, 1>(kind, args, stream);
+        return;
+    }
     switch (key) {
         case 256256: launch_tile<256, 256, 2, 4, 2>(kind, args, stream); break;   // 8 waves of 128 x 64
         case 256128: launch_tile<256, 128, 2, 2, 3>(kind, args, stream); break;   // waves 128 x 64

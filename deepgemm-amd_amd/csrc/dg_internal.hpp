@@ -75,12 +75,13 @@ struct Fp8GemmArgs {
     int64_t a_gs, b_gs, d_gs, c_gs;               // group strides
     int64_t sfa_sm, sfa_sk, sfa_gs;
     int64_t sfb_sn, sfb_sk, sfb_gs;
+    int32_t grid_limit;        // persistent kernels: workgroups to launch at most (the CU count)
 };
 
 struct TileConfig {
     int block_m;
     int block_n;
-    int variant = 1;   // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined
+    int variant = 1;   // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined, 4 = 2 persistent
 };
 
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.

@@ -155,6 +155,95 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
     return t;
 }
 
+// Persistent-scheduler form of decode_tile: tile `lt` of the launch's logical
+// tile sequence, or done = 1 past its end. Workgroup b of G takes
+// lt = xcd_remap(b, G) + i * G for i = 0, 1, ... (the reference's
+// get_next_block strides by the SM count the same way, scheduler/gemm.cuh:185-272).
+// For the masked layout the sequence only holds the m-blocks below each
+// group's masked_m: groups are walked in order, group g contributing
+// ceil(masked_m[g] / BM) x num_n_blocks tiles (scheduler/gemm.cuh:188-204).
+struct PTile : Tile {
+    int done;
+};
+
+template <int BM, int BN, int KIND, int NT>
+__device__ __forceinline__ PTile decode_tile_persistent(int lt, int m, int n, int num_groups,
+                                                        const int32_t* __restrict__ layout, int align_m,
+                                                        int zero_padding, int num_m_blocks, int num_n_blocks,
+                                                        uint16_t* zero_d, int64_t ldd, int* s_flag, int raster_gm) {
+    PTile t{};
+    t.done = 0;
+    int tile = lt;
+    int group_m_blocks = num_m_blocks;
+    if constexpr (KIND == kMasked) {
+        int g = 0;
+        for (; g < num_groups; ++g) {
+            const int rows = min(max(layout[g], 0), m);
+            const int cnt = (rows + BM - 1) / BM * num_n_blocks;
+            if (tile < cnt) {
+                group_m_blocks = (rows + BM - 1) / BM;
+                break;
+            }
+            tile -= cnt;
+        }
+        if (g == num_groups) {
+            t.done = 1;
+            return t;
+        }
+        t.g = g;
+    } else {
+        if (tile >= num_m_blocks * num_n_blocks) {
+            t.done = 1;
+            return t;
+        }
+    }
+    int mb, nb;
+    raster_tile(tile, group_m_blocks, num_n_blocks, raster_gm, mb, nb);
+    t.m0 = mb * BM;
+    t.n0 = nb * BN;
+    t.row_end = m;
+    t.active = 1;
+    if constexpr (KIND == kMasked) {
+        t.row_end = min(m, max(layout[t.g], 0));
+        t.expert = t.g;
+    } else if constexpr (KIND == kContiguous) {
+        t.expert = min(max(0, layout[t.m0]), num_groups - 1);
+        if (threadIdx.x == 0) *s_flag = 0;
+        __syncthreads();
+        for (int r = threadIdx.x; r < BM; r += NT)
+            if (t.m0 + r < m && layout[t.m0 + r] >= 0) *s_flag = 1;
+        __syncthreads();
+        t.active = *s_flag;
+    } else if constexpr (KIND == kPsum) {
+        int gi = 0, end = 0, aend = 0;
+        for (; gi < num_groups; ++gi) {
+            end = layout[gi];
+            aend = align_up(end, align_m);
+            if (t.m0 < aend) break;
+        }
+        if (gi == num_groups) {
+            t.active = 0;
+            return t;
+        }
+        end = min(end, m);
+        aend = min(aend, m);
+        t.expert = gi;
+        t.row_end = end;
+        t.pad_end = zero_padding ? aend : 0;
+        if (t.m0 >= end) {
+            t.active = 0;
+            if (zero_padding) {
+                const int r_hi = min(t.m0 + BM, aend);
+                for (int idx = threadIdx.x; idx < (r_hi - t.m0) * BN; idx += NT) {
+                    const int r = t.m0 + idx / BN, c = t.n0 + idx % BN;
+                    if (c < n) zero_d[(int64_t)r * ldd + c] = 0;
+                }
+            }
+        }
+    }
+    return t;
+}
+
 // Whether row `mrow` of this tile is stored (and whether as zeros).
 template <int KIND>
 __device__ __forceinline__ void row_predicate(const Tile& t, int m, const int32_t* __restrict__ layout, int mrow,

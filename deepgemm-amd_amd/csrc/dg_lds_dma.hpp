@@ -56,6 +56,18 @@ __device__ __forceinline__ int launder(int v) {
     return v;
 }
 
+// The kernel's first argument (a struct at offset 0 of the kernarg segment),
+// read afresh: the pointer is opaque, so the loads cannot be hoisted out of a
+// loop and their values are not kept live across it.
+template <typename T>
+__device__ __forceinline__ T reload_kernel_args() {
+    auto kp = (const __attribute__((address_space(4))) T*)(__builtin_amdgcn_kernarg_segment_ptr());
+    asm volatile("" : "+s"(kp));
+    T out;
+    __builtin_memcpy(&out, (const T*)kp, sizeof(T));
+    return out;
+}
+
 }  // namespace
 }  // namespace dev
 }  // namespace dgm

@@ -197,7 +197,9 @@ int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m
 /* Kernel/tile override for tests and tuning (no reference counterpart; the
  * reference's closest knobs are its JIT config printing and
  * set_block_size_multiple_of, csrc/apis/config.hpp:40-47). variant 1 = the
- * register-staged kernel, 2 = the LDS-pipelined kernel (both 32x32x64 MFMA);
+ * register-staged kernel, 2 = the LDS-pipelined kernel (both 32x32x64 MFMA),
+ * 4 = the pipelined kernel with persistent workgroups (one per CU, striding
+ * over the tile sequence like the reference's scheduler; 256 x 256 only);
  * variant 0 restores the heuristic. Only compiled tile shapes are accepted. */
 int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n);
 

@@ -310,6 +310,87 @@ def test_masked_edge_counts():
             assert not bool((d[i, :r].view(torch.int16) == SENTINEL).any())
 
 
+# ------------------------------------------------- persistent workgroups (variant 4)
+
+def _with_variant(v, fn):
+    try:
+        deep_gemm.set_tile_override(256, 256, variant=v)
+        out = fn()
+        torch.cuda.synchronize()
+        return out, deep_gemm.get_last_config()
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+
+
+@pytest.mark.parametrize('case', ['dense', 'dense_ragged', 'contiguous', 'masked', 'psum'])
+def test_persistent_equals_per_tile_launch(case):
+    """The persistent scheduler (grid = CU count, tile stride = grid, masked and
+    psum group walks) gives the same bits as one workgroup per tile: same tile
+    shape, same per-output K order; rows it must not touch stay untouched."""
+    print(f'persistent {case}', flush=True)
+    if case in ('dense', 'dense_ragged'):
+        m, n, k = (1024, 2048, 1024) if case == "dense" else (1300, 712, 896)
+        x = gen.dense_inputs(m, n, k, seed=91)
+        a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+
+        def run():
+            d = sentinel_bf16((m, n))
+            deep_gemm.fp8_gemm_nt(a, b, d)
+            return d
+    elif case == 'contiguous':
+        ms = [130, 100, 300, 0, 250, 1, 700]
+        aligned = [(mi + 127) // 128 * 128 for mi in ms]
+        x = gen.contiguous_inputs(ms, aligned, 384, 1024, seed=92)
+        a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+        mi_dev = gen.to_dev(x['m_indices'])
+
+        def run():
+            d = sentinel_bf16((sum(aligned), 384))
+            deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, mi_dev)
+            return d
+    elif case == 'masked':
+        x = gen.masked_inputs(6, 512, 512, 1024, seed=93)
+        x['masked_m'][:] = [0, 1, 256, 300, 512, 129]
+        a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+        mm = gen.to_dev(x['masked_m'])
+
+        def run():
+            d = sentinel_bf16((6, 512, 512))
+            deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, expected_m=256)
+            return d
+    else:
+        # 256-row tiles need a 256-row psum alignment
+        ms = [100, 0, 257, 64, 513]
+        align = 256
+        aligned = [(mi + align - 1) // align * align for mi in ms]
+        x = gen.contiguous_inputs(ms, aligned, 256, 512, seed=94)
+        a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+        ends, prev = [], 0
+        for mi in ms:
+            st = (prev + align - 1) // align * align
+            ends.append(st + mi)
+            prev = st + mi
+        psum = torch.tensor(ends, dtype=torch.int32, device=DEV)
+        m_pad = (ends[-1] + align - 1) // align * align
+
+        def run():
+            d = sentinel_bf16((m_pad, 256))
+            deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, psum, use_psum_layout=True,
+                                                       ensure_zero_padding=True)
+            return d
+    old_align = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    if case == 'psum':
+        deep_gemm.set_mk_alignment_for_contiguous_layout(256)
+    try:
+        ref, cfg_ref = _with_variant(2, run)
+        got, cfg = _with_variant(4, run)
+    finally:
+        deep_gemm.set_mk_alignment_for_contiguous_layout(old_align)
+    print(cfg_ref, '|', cfg, flush=True)
+    assert 'v4' in cfg
+    assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+
+
 # ----------------------------------------------------------------- SF layouts
 
 @pytest.mark.parametrize('mn,k,g', [(4096, 7168, 1), (4097, 128, 2), (300, 7296, 4)])
