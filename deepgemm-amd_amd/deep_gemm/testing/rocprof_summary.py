@@ -137,6 +137,21 @@ def summarize(args):
                                         for n, t in traffic.items()},
                    'calibration': calib}
 
+    mfma = None
+    if args.mfma:
+        # MFMA busy cycles summed over every SIMD, and GRBM_GUI_ACTIVE (the
+        # kernel's duration in clocks) summed over the XCDs.
+        busy = read_counters(args.mfma, 'SQ_VALU_MFMA_BUSY_CYCLES')
+        gui = read_counters(args.mfma, 'GRBM_GUI_ACTIVE')
+        bseq = gemm_sequence([(d, n, v) for d, (n, v) in busy.items()])
+        gseq2 = gemm_sequence([(d, n, v) for d, (n, v) in gui.items()])
+        psl, _ = phase_slices(len(names), args.pmc_warmup, args.pmc_steps)
+        mfma = {}
+        for name, sl, p in zip(names, psl, per):
+            b = sum(bseq[i][2] for i in sl) / len(sl)
+            cyc = sum(gseq2[i][2] for i in sl) / len(sl) / args.xcds
+            mfma[name] = {'mfma_busy_frac': b / (cyc * args.simds), 'clock_ghz': cyc / (p['avg_us'] * 1e3)}
+
     lines = []
     lines.append(f"# {bench['config']['workload']}\n")
     lines.append('Kernel durations from `rocprofv3 --kernel-trace --stats`, per-launch timing phase of '
@@ -176,6 +191,16 @@ def summarize(args):
             lines.append(f"| {n} | {t['fetch'] / 1e6:.1f} | {t['write'] / 1e6:.1f} | {t['total'] / 1e6:.1f} | "
                          f"{(a or 0) / 1e6:.1f} | {ratio} |")
         lines.append('')
+    if mfma:
+        lines.append('## MFMA utilization (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs))\n')
+        lines.append(f'{args.simds} SIMDs, GRBM_GUI_ACTIVE averaged over {args.xcds} XCDs; the clock is '
+                     'GRBM_GUI_ACTIVE over the traced kernel time (under the counter run, so approximate).\n')
+        lines.append('| launch | MFMA busy | clock GHz | MFMA busy x clock / 2.4 GHz |')
+        lines.append('|---|---|---|---|')
+        for n, v in mfma.items():
+            lines.append(f"| {n} | {100 * v['mfma_busy_frac']:.1f}% | {v['clock_ghz']:.2f} | "
+                         f"{100 * v['mfma_busy_frac'] * v['clock_ghz'] / 2.4:.1f}% |")
+        lines.append('')
     os.makedirs(os.path.dirname(os.path.abspath(args.md)), exist_ok=True)
     open(args.md, 'w').write('\n'.join(lines))
     if args.json:
@@ -184,6 +209,8 @@ def summarize(args):
                'kernel_us': {p['launch']: round(p['avg_us'], 2) for p in per}}
         if traffic:
             out.update(traffic)
+        if mfma:
+            out['mfma'] = {n: {k: round(x, 4) for k, x in v.items()} for n, v in mfma.items()}
         open(args.json, 'w').write(json.dumps(out, indent=1) + '\n')
     print('\n'.join(lines))
 
@@ -194,6 +221,9 @@ def main(argv=None):
     ap.add_argument('--trace', required=True)
     ap.add_argument('--fetch')
     ap.add_argument('--write')
+    ap.add_argument('--mfma', help='counter CSV of SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE')
+    ap.add_argument('--simds', type=int, default=1024)
+    ap.add_argument('--xcds', type=int, default=8)
     ap.add_argument('--copy-mib', type=float, default=1024)
     ap.add_argument('--warmup', type=int)
     ap.add_argument('--steps', type=int)
