@@ -280,7 +280,8 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     // Relative per-CU throughput of each kernel/tile, measured on MI355X at
     // M = 4096 over the DeepSeek-V3 shapes (pipelined 256 x 128 = 1.0).
     static const Cand cands[] = {
-        {2, 256, 256, 1, 1.32}, {2, 256, 128, 1, 1.00}, {2, 128, 256, 1, 0.97}, {2, 128, 128, 1, 0.80},
+        {2, 256, 256, 1, 1.32}, {2, 256, 192, 1, 1.16}, {2, 256, 128, 1, 1.00}, {2, 128, 256, 1, 0.97},
+        {2, 128, 128, 1, 0.80},
         {1, 128, 128, 2, 0.80}, {1, 128, 64, 3, 0.55}, {1, 64, 128, 3, 0.55}, {1, 64, 64, 4, 0.45}};
     int cus = 256;
     try { cus = num_sms_now(); } catch (const Error&) {}

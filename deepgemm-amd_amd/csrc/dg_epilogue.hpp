@@ -33,7 +33,8 @@ struct RowEpilogue {
     static constexpr int VPL = OUT_F32 ? 4 : 8;             // outputs per lane per store
     static constexpr int LPR = WN / VPL;                    // lanes per row
     static constexpr int RPI = 64 / LPR;                    // rows per store instruction
-    static_assert(64 % LPR == 0 && WM % RPI == 0, "row split");
+    static constexpr bool EXACT = (64 % LPR == 0);          // all 64 lanes busy (else lanes >= RPI * LPR idle)
+    static_assert(WN % VPL == 0 && LPR <= 64, "row split");
 
     // Rows staged per pass for a region of `bytes` (a multiple of 32, at most WM).
     static constexpr int rows_per_pass(int bytes) {
@@ -41,7 +42,12 @@ struct RowEpilogue {
         return r > WM ? WM : r;
     }
 
-    __device__ static int unit(int r, int u) { return u ^ (r & (UPR - 1)); }
+    // 16-byte unit u of staged row r: XOR swizzle when a row has a power-of-two
+    // number of units, else a rotation (both keep the unit inside its row).
+    __device__ static int unit(int r, int u) {
+        if constexpr ((UPR & (UPR - 1)) == 0) return u ^ (r & (UPR - 1));
+        else return (u + r) % UPR;
+    }
     __device__ static bool full_chunk(int n, int n_total) { return n + VPL <= n_total; }
 
     // fin: the wave's accumulators. region: the wave's LDS region (RPP rows).
@@ -97,8 +103,9 @@ struct RowEpilogue {
             // (LDS operations of one wave complete in order, so the reads see the
             // writes above and the next pass's writes follow these reads.)
 #pragma unroll
-            for (int it = 0; it < RPP / RPI; ++it) {
+            for (int it = 0; it < (RPP + RPI - 1) / RPI; ++it) {
                 const int r = it * RPI + lane / LPR;
+                if (!EXACT && (lane >= RPI * LPR || r >= RPP)) continue;
                 const int v0 = (lane % LPR) * VPL;             // first column (wave-local)
                 const int m = row0 + p0 + r;
                 const int n = col0 + v0;

@@ -74,7 +74,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     constexpr int SA_OFF = (BM + BN) * kBK;
     constexpr int SA_ROWS_PER_WAVE = BM / NW;  // SFA rows loaded by each wave (<= 64)
     constexpr int STAGE_BYTES = SA_OFF + NW * 256;
-    static_assert(WN <= 128 && 128 % WN == 0, "a wave's N range must sit in one 128-row SFB block");
+    // When every wave's N range sits in one 128-row SFB block, sa and sb fold into
+    // one factor per row; otherwise (e.g. 192-wide tiles) each 32-column sub-tile
+    // looks up its own block.
+    constexpr bool SPLIT_SB = !(BN % 128 == 0 && WN <= 128 && 128 % WN == 0);
     static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
     static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
 
@@ -119,7 +122,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     int npass = 1;
     int pass_expert[2] = {t.expert, t.expert};
     if constexpr (KIND == kContiguous && BM > 128) {
-        static_assert(BM == 256 && WM == 128, "two 128-row blocks, one per wave row");
+        static_assert(BM == 256 && 128 % WM == 0, "two 128-row blocks, each a whole number of wave rows");
         if (tid < 2) s_half_valid[tid] = 0;
         __syncthreads();
         for (int r = tid; r < BM; r += NT)
@@ -146,7 +149,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const int a_rows = min(BM, t.row_end - m0);
     const int b_rows = min(BN, p.n - n0);
     const int num_kb = (p.k + kBK - 1) / kBK;
-    const int my_group = (wn * WN) >> 7;
+    const int my_group = ((n0 & 127) + wn * WN) >> 7;
 
     // One pass of the tile: the whole K loop and the epilogue. Written as a lambda
     // called once (twice only for split contiguous tiles), since a loop around
@@ -163,7 +166,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     if constexpr (KIND == kMasked)
         wave_computes = __builtin_amdgcn_readfirstlane((int)(wm * WM < a_rows && p.m >= 0)) != 0;
     else
-        wave_computes = (npass == 1 || wm == pass) && p.m >= 0;
+        wave_computes = (npass == 1 || (wm * WM) >> 7 == pass) && p.m >= 0;
     const uint8_t* __restrict__ b_base = p.b + (int64_t)expert * p.b_gs + (int64_t)n0 * p.ldb;
     if (pass > 0) __syncthreads();   // every wave is done with the stage ring and s_sfb of the previous pass
     {
@@ -276,17 +279,28 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // 32-row slice, double-buffered so slice i + 1 is read while slice i computes.
     i32x8 opB[SN][2], opA[2][2];
     float sa_cur[SM];
+    float scl[SPLIT_SB ? SM : 1][SPLIT_SB ? SN : 1];
     // sa * sb of the lane's rows for K block kb (read at the top of the block's
     // compute; the stage slot is refilled only after the next barrier).
     auto load_scales = [&](int kb) {
         const uint8_t* sbase = smem + (kb % STAGES) * STAGE_BYTES;
-        const float sb = s_sfb[my_group][kb];
 #pragma unroll
         for (int i = 0; i < SM; ++i) {
             const int r = wm * WM + i * 32 + lrow;
-            sa_cur[i] = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
-                                                        (r % SA_ROWS_PER_WAVE) * 4) * sb;
+            const float sa = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
+                                                             (r % SA_ROWS_PER_WAVE) * 4);
+            if constexpr (SPLIT_SB) {
+#pragma unroll
+                for (int j = 0; j < SN; ++j)
+                    scl[i][j] = sa * s_sfb[((n0 & 127) + wn * WN + j * 32) >> 7][kb];
+            } else {
+                sa_cur[i] = sa * s_sfb[my_group][kb];
+            }
         }
+    };
+    auto scale_of = [&](int i, int j) {
+        if constexpr (SPLIT_SB) return scl[i][j];
+        else return sa_cur[i];
     };
     auto load_stage_frags = [&](int kb) {
         const uint8_t* sbase = smem + (kb % STAGES) * STAGE_BYTES;
@@ -383,13 +397,13 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                 const int pi = j > 0 ? i : i - 1;
                 if (pi >= 0) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) fin[pi][pj][e] = __builtin_fmaf(sa_cur[pi], acc[pj][e], fin[pi][pj][e]);
+                    for (int e = 0; e < 16; ++e) fin[pi][pj][e] = __builtin_fmaf(scale_of(pi, pj), acc[pj][e], fin[pi][pj][e]);
                 }
             }
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-            fin[SM - 1][SN - 1][e] = __builtin_fmaf(sa_cur[SM - 1], acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
+            fin[SM - 1][SN - 1][e] = __builtin_fmaf(scale_of(SM - 1, SN - 1), acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
         }
     }
 
@@ -437,14 +451,14 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                         if (pi >= 0) {
 #pragma unroll
                             for (int e = 0; e < 16; ++e)
-                                fin[pi][pj][e] = __builtin_fmaf(sa_cur[pi], acc[pj][e], fin[pi][pj][e]);
+                                fin[pi][pj][e] = __builtin_fmaf(scale_of(pi, pj), acc[pj][e], fin[pi][pj][e]);
                         }
                     }
                 }
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
                     fin[SM - 1][SN - 1][e] =
-                        __builtin_fmaf(sa_cur[SM - 1], acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
+                        __builtin_fmaf(scale_of(SM - 1, SN - 1), acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
             }
         }
     }
@@ -537,8 +551,8 @@ void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
 }  // namespace
 
 bool fp8_1d2d_v2_tile_supported(int bm, int bn) {
-    return (bm == 256 && bn == 256) || (bm == 256 && bn == 128) || (bm == 128 && bn == 256) ||
-           (bm == 128 && bn == 128);
+    return (bm == 256 && bn == 256) || (bm == 256 && bn == 192) || (bm == 256 && bn == 128) ||
+           (bm == 128 && bn == 256) || (bm == 128 && bn == 128);
 }
 
 void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args, hipStream_t stream) {
@@ -551,6 +565,7 @@ void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8Gemm
     switch (key) {
         case 256256: launch_tile<256, 256, 2, 4, 2>(kind, args, stream); break;   // 8 waves of 128 x 64
         case 256128: launch_tile<256, 128, 2, 2, 3>(kind, args, stream); break;   // waves 128 x 64
+        case 256192: launch_tile<256, 192, 4, 2, 2>(kind, args, stream); break;   // 8 waves of 64 x 96
         case 128256: launch_tile<128, 256, 2, 4, 3>(kind, args, stream); break;   // 8 waves of 64 x 64
         case 128128: launch_tile<128, 128, 2, 2, 4>(kind, args, stream); break;   // waves 64 x 64
         default: DG_UNSUPPORTED("tile shape not compiled for the pipelined FP32-scale FP8 kernel");

@@ -86,7 +86,7 @@ def test_all_tiles_bitwise_equal(m, n, k):
     outs = []
     try:
         for v, bm, bn in ((1, 64, 64), (1, 64, 128), (1, 128, 64), (1, 128, 128),
-                          (2, 128, 128), (2, 128, 256), (2, 256, 128), (2, 256, 256)):
+                          (2, 128, 128), (2, 128, 256), (2, 256, 128), (2, 256, 192), (2, 256, 256)):
             deep_gemm.set_tile_override(bm, bn, variant=v)
             d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
             deep_gemm.fp8_gemm_nt(a, b, d)
@@ -184,7 +184,7 @@ def test_k_zero_and_empty():
 
 # ----------------------------------------------------------------- grouped
 
-CONTIG_TILES = [None, (2, 256, 256), (2, 128, 256), (1, 128, 128)]
+CONTIG_TILES = [None, (2, 256, 256), (2, 256, 192), (2, 128, 256), (1, 128, 128)]
 
 
 @pytest.mark.parametrize('tile', CONTIG_TILES)
