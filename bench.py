@@ -6,13 +6,21 @@ the DeepSeek-V3 (N, K) sweep {(2112,7168), (24576,1536), (7168,16384),
 output. One step = one call per shape (5 launches). `value` is total
 algorithmic FLOPs / wall time of the timed steps (inputs resident in HBM).
 
+Each launch has 8 rotating buffer sets (copies of its inputs and outputs) and
+step s runs on set s % 8, so no launch finds its operands in L2 or the 256 MB
+Infinity Cache. Steps are replayed from HIP graphs captured once (the library
+launches into a capturing stream like any other), which takes the Python call
+overhead out of the timed region; --eager launches from Python instead.
+
 Other workloads (`--workload`): dense_acc (FP32 C += A.B^T), contiguous
 (config 3, 8 experts, 32768 tokens), masked (config 4, 16 experts, max_m 256),
-fp8fp4 (config 5).
+fp8fp4 (config 5), cast (the fused per-token FP8 activation cast that produces
+A and its MN-major SFA for these GEMMs; HBM-bound, reported in GB/s).
 
 Prints one JSON line. `roofline` is computed from per-launch durations measured
-live with HIP events on the launch stream; `cpu_baseline` times the CPU FP32
-dequantize-then-matmul reference (oracle/) on a bounded sample.
+live with HIP events on the launch stream; `cpu_baseline` times the oracle/
+restatement on the host on a bounded sample (the FP32 dequantize-then-matmul
+for the GEMMs, the numpy quantizer for the cast).
 """
 import argparse
 import json
@@ -31,7 +39,8 @@ DENSE_NK = [(2112, 7168), (24576, 1536), (7168, 16384), (4096, 7168), (7168, 204
 # written by deep_gemm.testing.rocprof_summary), per workload.
 PROFILE_NAMES = {'dense': 'fp8_gemm_nt_dense_m4096', 'dense_acc': 'fp8_gemm_nt_dense_acc_m4096',
                  'contiguous': 'm_grouped_fp8_gemm_nt_contiguous_e8_t32768',
-                 'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096'}
+                 'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096',
+                 'cast': 'per_token_cast_to_fp8_bf16'}
 
 
 def parse():
@@ -40,8 +49,10 @@ def parse():
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--workload', default='dense',
-                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4'])
+                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--rotate', type=int, default=8, help='rotating buffer sets per launch')
+    ap.add_argument('--eager', action='store_true', help='launch from Python instead of replaying HIP graphs')
     ap.add_argument('--cpu-sample-m', type=int, default=512)
     ap.add_argument('--calibrate-copy-mib', type=int, default=0,
                     help='first run torch.neg over this many MiB of float32 (a plain copy kernel of known '
@@ -56,10 +67,22 @@ def log(*a):
 # ---------------------------------------------------------------- workloads
 
 class Launch:
-    """One GEMM launch of the workload with its algorithmic FLOPs and bytes."""
+    """One launch of the workload with its algorithmic FLOPs and bytes. `mk()`
+    returns a callable bound to a fresh copy of the launch's inputs and outputs
+    (one rotating buffer set)."""
 
-    def __init__(self, name, fn, flops, nbytes):
-        self.name, self.fn, self.flops, self.nbytes = name, fn, flops, nbytes
+    def __init__(self, name, mk, flops, nbytes):
+        self.name, self.mk, self.flops, self.nbytes = name, mk, flops, nbytes
+
+
+def _twin(x):
+    """Copy of a tensor (or of each tensor of a tuple) with the same strides."""
+    import torch
+    if isinstance(x, (tuple, list)):
+        return tuple(_twin(t) for t in x)
+    out = torch.empty_strided(tuple(x.shape), x.stride(), dtype=x.dtype, device=x.device)
+    out.copy_(x)
+    return out
 
 
 def _quant_a(m, k, gen, dev):
@@ -88,14 +111,19 @@ def make_dense(acc: bool):
         b = _quant_b(n, k, gen, dev)
         if acc:
             d = (torch.randn((m, n), generator=gen) * 32).to(dev)
-            fn = (lambda a=a, b=b, d=d: deep_gemm.fp8_gemm_nt(a, b, d, c=d))
+
+            def mk(a=a, b=b, d=d):
+                a2, b2, d2 = _twin(a), _twin(b), _twin(d)
+                return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2, c=d2)
             out_bytes = 8 * m * n
         else:
-            d = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-            fn = (lambda a=a, b=b, d=d: deep_gemm.fp8_gemm_nt(a, b, d))
+            def mk(a=a, b=b, m=m, n=n):
+                a2, b2 = _twin(a), _twin(b)
+                d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+                return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2)
             out_bytes = 2 * m * n
         nbytes = m * k + n * k + 4 * m * ((k + 127) // 128) + 4 * ((n + 127) // 128) * ((k + 127) // 128) + out_bytes
-        launches.append(Launch(f'n{n}_k{k}', fn, 2 * m * n * k, nbytes))
+        launches.append(Launch(f'n{n}_k{k}', mk, 2 * m * n * k, nbytes))
     cfg = {'workload': 'fp8_gemm_nt M=4096 DeepSeek-V3 (N,K) sweep' + (' FP32 C-accumulate' if acc else ''),
            'm': m, 'nk': DENSE_NK, 'out': 'f32 (D=C+AB^T)' if acc else 'bf16',
            'recipe': '1x128 A / 128x128 B FP32 scales'}
@@ -129,10 +157,12 @@ def make_contiguous():
         bs = torch.empty((g, (n + 127) // 128, (k + 127) // 128), device=dev)
         for i in range(g):
             bq[i], bs[i] = _quant_b(n, k, gen, dev)
-        d = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
-        fn = (lambda a=a, b=(bq, bs), d=d: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, idx))
+        def mk(a=a, b=(bq, bs), n=n):
+            a2, b2 = _twin(a), _twin(b)
+            d2 = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
+            return lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a2, b2, d2, idx)
         nbytes = m_pad * k + g * n * k + 2 * m_pad * n + 4 * m_pad * ((k + 127) // 128) + 4 * m_pad
-        launches.append(Launch(f'n{n}_k{k}', fn, 2 * total * n * k, nbytes))
+        launches.append(Launch(f'n{n}_k{k}', mk, 2 * total * n * k, nbytes))
     cfg = {'workload': 'm_grouped_fp8_gemm_nt_contiguous 8 experts 32768 tokens Dirichlet(1)',
            'tokens_per_expert': [int(v) for v in ms], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)]}
     return launches, cfg, 'mfma'
@@ -159,11 +189,13 @@ def make_masked():
             aq[i], as_[i] = _quant_a(max_m, k, gen, dev)
             as_[i, int(masked[i]):] = 0
             bq[i], bs[i] = _quant_b(n, k, gen, dev)
-        d = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
-        fn = (lambda a=(aq, as_), b=(bq, bs), d=d: deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, 128))
+        def mk(a=(aq, as_), b=(bq, bs), n=n):
+            a2, b2 = _twin(a), _twin(b)
+            d2 = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
+            return lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked(a2, b2, d2, mm, 128)
         nbytes = g * n * k + sum_m * k + 2 * sum_m * n + 4 * sum_m * ((k + 127) // 128) + \
             4 * g * ((n + 127) // 128) * ((k + 127) // 128)
-        launches.append(Launch(f'n{n}_k{k}', fn, 2 * sum_m * n * k, nbytes))
+        launches.append(Launch(f'n{n}_k{k}', mk, 2 * sum_m * n * k, nbytes))
     cfg = {'workload': 'm_grouped_fp8_gemm_nt_masked 16 experts max_m=256 masked_m~U[96,160]',
            'masked_m': masked.tolist(), 'nk': [(4096, 7168), (7168, 2048)]}
     return launches, cfg, 'hbm'
@@ -183,12 +215,35 @@ def make_fp8fp4():
     # the GEMM kernel alone, tests/test_fp8_fp4.py:84-86,100).
     a = (a[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(a[1]))
     b = (b[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(b[1]))
-    d = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    fn = (lambda: deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, 128), recipe_b=(1, 32)))
+
+    def mk():
+        a2, b2 = _twin(a), _twin(b)
+        d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        return lambda: deep_gemm.fp8_fp4_gemm_nt(a2, b2, d2, recipe_a=(1, 128), recipe_b=(1, 32))
     nbytes = m * k + n * k // 2 + 4 * m * (k // 128) + 4 * n * (k // 32) + 2 * m * n
     cfg = {'workload': 'fp8_fp4_gemm_nt M=4096 N=K=7168, A e4m3 1x128 UE8M0, B e2m1 1x32 UE8M0', 'm': m, 'n': n,
            'k': k}
-    return [Launch('m4096_n7168_k7168', fn, 2 * m * n * k, nbytes)], cfg, 'mfma'
+    return [Launch('m4096_n7168_k7168', mk, 2 * m * n * k, nbytes)], cfg, 'mfma'
+
+
+CAST_MK = [(4096, 7168), (4096, 16384), (4096, 1536), (32768, 7168)]
+
+
+def make_cast():
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator().manual_seed(0)
+    launches = []
+    for m, k in CAST_MK:
+        x = torch.randn((m, k), generator=gen).bfloat16().to(dev)
+        def mk(x=x):
+            x2 = _twin(x)
+            return lambda: deep_gemm.per_token_cast_to_fp8_mn_major(x2, use_ue8m0=False)
+        nbytes = 2 * m * k + m * k + 4 * m * ((k + 127) // 128)
+        launches.append(Launch(f'm{m}_k{k}', mk, 0, nbytes))
+    cfg = {'workload': 'per_token_cast_to_fp8 bf16 -> e4m3 + MN-major FP32 1x128 SFA', 'mk': CAST_MK}
+    return launches, cfg, 'hbm'
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -199,6 +254,18 @@ def cpu_baseline(workload: str, sample_m: int):
     import torch
     from oracle import gemm as ogemm, quant as oquant
     cores = len(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else os.cpu_count()
+    if workload == 'cast':
+        rows = 32 * sample_m   # the cast is far cheaper per row than a GEMM row
+        nbytes, secs = 0, 0.0
+        for _, k in CAST_MK:
+            x = torch.randn((rows, k), generator=torch.Generator().manual_seed(1)).bfloat16().float().numpy()
+            t0 = time.perf_counter()
+            oquant.per_token_cast_to_fp8(x, use_ue8m0=False)
+            secs += time.perf_counter() - t0
+            nbytes += 3 * rows * k + 4 * rows * ((k + 127) // 128)
+        return {'value': round(nbytes / secs / 1e9, 3), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
+                'sample': f'M={rows} rows of each (M,K) shape: the oracle\'s numpy per-token cast '
+                          f'(single-threaded numpy), {secs:.1f} s total'}
     rng = np.random.default_rng(0)
     nk = DENSE_NK if workload in ('dense', 'dense_acc') else [(4096, 7168), (7168, 2048)]
     flops, secs = 0, 0.0
@@ -245,7 +312,7 @@ def main():
     import deep_gemm
     torch.cuda.set_device(0)
     makers = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
-              'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4}
+              'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast}
     if args.calibrate_copy_mib > 0:
         x = torch.randn(args.calibrate_copy_mib * 1024 * 256, device='cuda:0')
         y = torch.empty_like(x)
@@ -254,49 +321,98 @@ def main():
         torch.cuda.synchronize()
         del x, y
     launches, cfg, bound = makers[args.workload]()
+    rot = args.rotate
+    # Rotating buffer sets: fns[i][r] runs launch i on its own copy r of the
+    # inputs and outputs, so consecutive launches never find their operands in
+    # L2 or the Infinity Cache (the sets of a step span well over 288 MB).
+    fns = [[l.mk() for _ in range(rot)] for l in launches]
     torch.cuda.synchronize()
-    log(f'workload {args.workload}: {len(launches)} launches per step')
+    log(f'workload {args.workload}: {len(launches)} launches per step, {rot} rotating buffer sets')
 
-    for _ in range(args.warmup):
-        for l in launches:
-            l.fn()
+    # One eager pass over every set: library initialisation, and the kernel
+    # configuration each launch resolves to.
+    configs = []
+    for i in range(len(launches)):
+        for r in range(rot):
+            fns[i][r]()
+        configs.append(deep_gemm.get_last_config())
     torch.cuda.synchronize()
 
-    # Per-launch durations: HIP events on the launch stream (torch's current stream,
-    # which the library launches on) around each repetition, with L2 and the 256 MB
-    # Infinity Cache flushed before it by zeroing a 512 MiB buffer, as the
-    # reference's bench_kineto flushes L2 (deep_gemm/testing/bench.py:76-104), so
-    # operands come from HBM.
+    # HIP graphs (the library records into a capturing stream like any other):
+    # one per launch over its sets (per-launch timing) and one per set over all
+    # launches (one step). Replays take the Python launch overhead out of both
+    # timed regions; --eager launches from Python instead.
+    if not args.eager:
+        launch_graphs, step_graphs = [], []
+        for i in range(len(launches)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for r in range(rot):
+                    fns[i][r]()
+            launch_graphs.append(g)
+        for r in range(rot):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(len(launches)):
+                    fns[i][r]()
+            step_graphs.append(g)
+        torch.cuda.synchronize()
+
+    def run_launch(i):
+        if args.eager:
+            for r in range(rot):
+                fns[i][r]()
+        else:
+            launch_graphs[i].replay()
+
+    def run_step(sidx):
+        if args.eager:
+            for i in range(len(launches)):
+                fns[i][sidx % rot]()
+        else:
+            step_graphs[sidx % rot].replay()
+
+    # Per-launch durations: HIP events on the launch stream (torch's current
+    # stream, which the library and graph replays launch on) around the launch
+    # run over all of its sets, with L2 and the 256 MB Infinity Cache flushed
+    # before it, as the reference's bench_kineto flushes L2
+    # (deep_gemm/testing/bench.py:76-104), so operands come from HBM. The flush
+    # READS a 512 MiB buffer instead of zero-filling one: a fill leaves up to
+    # 288 MB of dirty lines in L2 and the memory-side Infinity Cache whose
+    # write-back then lands inside the next timed kernel (up to 30% of an
+    # HBM-bound launch here); a read evicts the operands without that backlog.
     stream = torch.cuda.current_stream()
-    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device='cuda:0')
-    per, configs = [], []
-    for l in launches:
-        reps = max(5, args.steps)
+    flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device='cuda:0')
+    reps = max(5, args.steps)
+    per = []
+    for i, l in enumerate(launches):
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
         for e0, e1 in evs:
-            flush.zero_()
+            torch.sum(flush, dtype=torch.int64)
             e0.record(stream)
-            l.fn()
+            run_launch(i)
             e1.record(stream)
         torch.cuda.synchronize()
-        us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / reps
+        us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / (reps * rot)
         per.append(us)
-        configs.append(deep_gemm.get_last_config())
         log(f'  {l.name}: {us:8.1f} us  {l.flops / us / 1e6:7.1f} TFLOPS  {l.nbytes / us / 1e3:7.1f} GB/s  '
-            f'[{deep_gemm.get_last_config()}]')
-
+            f'[{configs[i]}]')
     del flush
+
+    for w in range(args.warmup):
+        run_step(w)
     # Whole-job timed region: K steps, synchronized on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        for l in launches:
-            l.fn()
+    for sidx in range(args.steps):
+        run_step(sidx)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     total_flops = sum(l.flops for l in launches) * args.steps
     total_bytes = sum(l.nbytes for l in launches)
     value = total_flops / elapsed / 1e12
+    if total_flops == 0:   # a byte-moving workload (cast): GB/s
+        value = total_bytes * args.steps / elapsed / 1e9
 
     kernel_us = sum(per)
     if bound == 'mfma':
@@ -311,8 +427,9 @@ def main():
     roofline = {'bound': bound, 'achieved': round(achieved, 2), 'peak': peak, 'unit': unit,
                 'frac': round(achieved / peak, 4), 'traffic': traffic,
                 'per': f'one step = {len(launches)} launch(es), one per shape; achieved = algorithmic '
-                       f'{"FLOPs" if bound == "mfma" else "bytes"} of the step / sum of per-launch durations; '
-                       f'traffic = calibrated HBM bytes (FETCH_SIZE + WRITE_SIZE) of the step',
+                       f'{"FLOPs" if bound == "mfma" else "bytes"} of the step / sum of per-launch durations '
+                       f'(each the event time of {rot} back-to-back launches on rotating buffer sets after a '
+                       f'cache flush, / {rot}); traffic = calibrated HBM bytes (FETCH_SIZE + WRITE_SIZE) of the step',
                 'traffic_source': traffic_note,
                 'kernel': sorted({c.split(' kind=')[0] for c in configs}),
                 'launch_config': {l.name: c for l, c in zip(launches, configs)},
@@ -320,10 +437,12 @@ def main():
                 'per_launch_us': {l.name: round(u, 2) for l, u in zip(launches, per)},
                 'per_launch_tflops': {l.name: round(l.flops / u / 1e6, 1) for l, u in zip(launches, per)},
                 'per_launch_gbs': {l.name: round(l.nbytes / u / 1e3, 1) for l, u in zip(launches, per)}}
+    cast = args.workload == 'cast'
     out = {
-        'metric': 'FP8 block-scaled GEMM TFLOPS + % of MI355X FP8 MFMA peak, DSV3 shapes',
+        'metric': ('FP8 per-token activation cast GB/s (bf16 -> e4m3 + 1x128 SFA)' if cast else
+                   'FP8 block-scaled GEMM TFLOPS + % of MI355X FP8 MFMA peak, DSV3 shapes'),
         'value': round(value, 2),
-        'unit': 'TFLOPS',
+        'unit': 'GB/s' if cast else 'TFLOPS',
         'n_gpus': 1,
         'steps': args.steps,
         'warmup': args.warmup,
@@ -331,9 +450,12 @@ def main():
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
-        'dtype': 'e4m3 (fp32 accumulate)' if args.workload != 'fp8fp4' else 'e4m3 x e2m1 (fp32 accumulate)',
+        'dtype': ('bf16 -> e4m3' if cast else
+                  'e4m3 (fp32 accumulate)' if args.workload != 'fp8fp4' else 'e4m3 x e2m1 (fp32 accumulate)'),
         'data': 'synthetic (seeded randn, bf16 -> quantized)',
         'config': cfg,
+        'timing': {'launch': 'eager (Python)' if args.eager else 'hipGraph replay', 'rotating_sets': rot,
+                   'per_launch_reps': reps},
         'roofline': roofline,
     }
     if not args.no_cpu_baseline:

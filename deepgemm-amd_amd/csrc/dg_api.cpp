@@ -617,6 +617,41 @@ void pack_impl(const dg_tensor* sf_, const dg_tensor* out_, hipStream_t stream) 
     launch_sf_pack_ue8m0(args, stream);
 }
 
+void cast_impl(const dg_tensor* x_, const dg_tensor* q_, const dg_tensor* sf_, int32_t gran_k, int32_t use_ue8m0,
+               hipStream_t stream) {
+    const View x = view(x_, "x"), q = view(q_, "q"), sf = view(sf_, "sf");
+    DG_CHECK(x.dim() == 2 && q.dim() == 2 && sf.dim() == 2);
+    DG_CHECK(x.dtype() == DG_BF16 && q.dtype() == DG_E4M3);
+    DG_CHECK(x.on_device() && q.on_device() && sf.on_device());
+    DG_CHECK(gran_k == 32 || gran_k == 64 || gran_k == 128);
+    const int64_t m = x.size(0), n = x.size(1);
+    DG_CHECK(q.size(0) == m && q.size(1) == n);
+    DG_CHECK(x.stride(-1) == 1 && q.stride(-1) == 1);
+    const int64_t groups = ceil_div(n, (int64_t)gran_k);
+    const bool packed = sf.dtype() == DG_I32;
+    if (packed) {
+        DG_CHECK(use_ue8m0);
+        DG_CHECK(sf.size(0) == m && sf.size(1) == ceil_div(groups, (int64_t)4));
+    } else {
+        DG_CHECK(sf.dtype() == DG_F32);
+        DG_CHECK(sf.size(0) == m && sf.size(1) == groups);
+    }
+    DG_CHECK(m < ((int64_t)1 << 31) && n < ((int64_t)1 << 27));
+    CastArgs a{};
+    a.x = static_cast<const uint16_t*>(x.data());
+    a.ldx = x.stride(0);
+    a.q = static_cast<uint8_t*>(const_cast<void*>(q.data()));
+    a.ldq = q.stride(0);
+    a.sf = const_cast<void*>(sf.data());
+    a.sf_sm = sf.stride(0), a.sf_sk = sf.stride(1);
+    a.m = (int32_t)m, a.n = (int32_t)n, a.gran = gran_k, a.ue8m0 = use_ue8m0 != 0, a.packed = packed;
+    launch_per_token_cast(a, stream);
+    char buf[160];
+    std::snprintf(buf, sizeof(buf), "per_token_cast kind=%s gran_k=%d ue8m0=%d m=%lld n=%lld",
+                  packed ? "packed" : "f32", gran_k, (int)a.ue8m0, (long long)m, (long long)n);
+    t_last_config = buf;
+}
+
 }  // namespace
 }  // namespace dgm
 
@@ -691,6 +726,11 @@ int dg_plan_sf_transform(const dg_tensor* sf, int32_t mn, int32_t k, const int32
         DG_CHECK(kind != nullptr);
         *kind = plan_sf(sf, mn, k, recipe3, recipe2, num_groups, is_sfa, disable_ue8m0_cast);
     });
+}
+
+int dg_per_token_cast_to_fp8(const dg_tensor* x, const dg_tensor* q, const dg_tensor* sf, int32_t gran_k,
+                             int32_t use_ue8m0, void* stream) {
+    return guarded([&] { cast_impl(x, q, sf, gran_k, use_ue8m0, static_cast<hipStream_t>(stream)); });
 }
 
 int dg_set_num_sms(int32_t num_sms) {

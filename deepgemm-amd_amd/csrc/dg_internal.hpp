@@ -148,6 +148,18 @@ struct SfPackArgs {
 };
 void launch_sf_pack_ue8m0(const SfPackArgs& args, hipStream_t stream);
 
+// Fused per-token FP8 cast (dg_cast.hip).
+struct CastArgs {
+    const uint16_t* x;         // bf16 [m, n]
+    int64_t ldx;               // elements
+    uint8_t* q;                // e4m3 [m, n]
+    int64_t ldq;               // bytes
+    void* sf;                  // f32 [m, ceil(n / gran)] or packed int32 [m, ceil(ceil(n / gran) / 4)]
+    int64_t sf_sm, sf_sk;      // SF strides in elements (any layout)
+    int32_t m, n, gran, ue8m0, packed;
+};
+void launch_per_token_cast(const CastArgs& args, hipStream_t stream);
+
 // D <- C (or zeros when c is null), used by the K == 0 early return.
 void launch_fill_or_copy(void* d, const void* c, int32_t rows, int32_t cols, int32_t groups,
                          int64_t ldd, int64_t d_gs, int64_t ldc, int64_t c_gs, int elem_bytes,

@@ -312,3 +312,45 @@ def get_last_config() -> str:
 from . import testing  # noqa: E402
 from . import utils  # noqa: E402
 from .utils import *  # noqa: E402,F401,F403
+
+
+# ------------------------------------------------------------------ activation cast
+
+def _cast_on_device(x: torch.Tensor) -> bool:
+    return x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(-1) == 1 and x.size(1) < (1 << 27)
+
+
+def per_token_cast_to_fp8(x: torch.Tensor, use_ue8m0: bool, gran_k: int = 128,
+                          use_packed_ue8m0: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """[m, n] -> (e4m3 [m, n], float32 SF [m, ceil(n / gran_k)] or packed int32 UE8M0 words)
+    (reference deep_gemm/utils/math.py:26-49). BF16 device tensors take the fused HIP
+    kernel (one HBM pass); anything else takes the torch ops of deep_gemm.utils.math."""
+    if not _cast_on_device(x) or gran_k not in (32, 64, 128):
+        return utils.math.per_token_cast_to_fp8(x, use_ue8m0, gran_k, use_packed_ue8m0)
+    assert not use_packed_ue8m0 or use_ue8m0
+    m, n = x.shape
+    groups = (n + gran_k - 1) // gran_k
+    q = torch.empty((m, n), dtype=torch.float8_e4m3fn, device=x.device)
+    if use_packed_ue8m0:
+        sf = torch.empty((m, (groups + 3) // 4), dtype=torch.int32, device=x.device)
+    else:
+        sf = torch.empty((m, groups), dtype=torch.float32, device=x.device)
+    _check(_lib.dg_per_token_cast_to_fp8(_ref(_desc(x)), _ref(_desc(q)), _ref(_desc(sf)), int(gran_k),
+                                         int(bool(use_ue8m0)), _ffi.stream_of(x)))
+    return q, sf
+
+
+def per_token_cast_to_fp8_mn_major(x: torch.Tensor, use_ue8m0: bool,
+                                   gran_k: int = 128) -> Tuple[torch.Tensor, torch.Tensor]:
+    """per_token_cast_to_fp8 with the scales written straight into the MN-major
+    TMA-aligned layout (strides (1, align(m, 4))), the fused form of
+    per_token_cast_to_fp8 + get_mn_major_tma_aligned_tensor. No reference counterpart."""
+    assert _cast_on_device(x), 'needs a 2-D bf16 device tensor with unit stride along K'
+    m, n = x.shape
+    groups = (n + gran_k - 1) // gran_k
+    am = (m + 3) // 4 * 4
+    q = torch.empty((m, n), dtype=torch.float8_e4m3fn, device=x.device)
+    sf = torch.empty_strided((m, groups), (1, am), dtype=torch.float32, device=x.device)
+    _check(_lib.dg_per_token_cast_to_fp8(_ref(_desc(x)), _ref(_desc(q)), _ref(_desc(sf)), int(gran_k),
+                                         int(bool(use_ue8m0)), _ffi.stream_of(x)))
+    return q, sf

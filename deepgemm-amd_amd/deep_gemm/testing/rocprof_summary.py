@@ -6,9 +6,10 @@ Two inputs are understood:
   * `<prefix>_counter_collection.csv` of `rocprofv3 --pmc <COUNTER> --output-format csv`
     (one row per dispatch and counter).
 
-GEMM dispatches are mapped to bench.py's launch names by dispatch order: bench.py
-runs `warmup` steps of all launches, then `max(5, steps)` back-to-back repetitions
-of each launch in turn (the per-launch timing phase), then `steps` timed steps.
+Library dispatches are mapped to bench.py's launch names by dispatch order:
+bench.py first runs every launch once on each of its R rotating buffer sets,
+then, launch by launch, `max(5, steps)` repetitions of R back-to-back launches
+(the per-launch timing phase), then `warmup` and `steps` steps of all launches.
 Only the per-launch phase is summarised, so each figure belongs to one shape.
 
 HBM traffic: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what the
@@ -30,11 +31,13 @@ import os
 import sys
 
 GEMM_KEYS = ('fp8_gemm_1d2d', 'fp8_fp4_gemm', 'fp8_gemm_1d2d_pipe')
+CAST_KEYS = ('per_token_cast_kernel',)   # the cast workload's kernel (GEMM workloads also cast while setting up)
 COPY_KEY = 'neg_kernel'
+_KEYS = GEMM_KEYS
 
 
 def _is_gemm(name: str) -> bool:
-    return any(k in name for k in GEMM_KEYS)
+    return any(k in name for k in _KEYS)
 
 
 def _short(name: str) -> str:
@@ -51,12 +54,12 @@ def _short(name: str) -> str:
     return name
 
 
-def phase_slices(num_launches: int, warmup: int, steps: int):
-    """Index ranges, within the GEMM dispatch sequence, of each launch's
-    per-launch timing repetitions."""
-    reps = max(5, steps)
-    base = warmup * num_launches
-    return [range(base + i * reps, base + (i + 1) * reps) for i in range(num_launches)], reps
+def phase_slices(num_launches: int, steps: int, rot: int):
+    """Index ranges, within the library dispatch sequence, of each launch's
+    per-launch timing dispatches (repetitions x rotating sets)."""
+    per = max(5, steps) * rot
+    base = rot * num_launches
+    return [range(base + i * per, base + (i + 1) * per) for i in range(num_launches)], per
 
 
 def read_trace(path):
@@ -84,19 +87,22 @@ def gemm_sequence(items):
 
 
 def summarize(args):
+    global _KEYS
     bench = json.loads(open(args.bench_json).read().strip().splitlines()[-1])
     roof = bench['roofline']
+    _KEYS = CAST_KEYS if roof.get('kernel') == ['per_token_cast'] else GEMM_KEYS
     names = list(roof['per_launch_us'].keys())
     warmup = args.warmup if args.warmup is not None else bench['warmup']
     steps = args.steps if args.steps is not None else bench['steps']
-    slices, reps = phase_slices(len(names), warmup, steps)
+    rot = bench.get('timing', {}).get('rotating_sets', 1)
+    slices, reps = phase_slices(len(names), steps, rot)
 
     trace = read_trace(args.trace)
     seq = gemm_sequence([(int(r['Dispatch_Id']), r['Kernel_Name'], r) for r in trace])
-    expected = (warmup + steps) * len(names) + reps * len(names)
+    expected = (rot + warmup + steps) * len(names) + reps * len(names)
     if len(seq) != expected:
-        sys.exit(f'expected {expected} GEMM dispatches (warmup {warmup}, steps {steps}, '
-                 f'{len(names)} launches), found {len(seq)}')
+        sys.exit(f'expected {expected} library dispatches (warmup {warmup}, steps {steps}, '
+                 f'{rot} rotating sets, {len(names)} launches), found {len(seq)}')
     per = []
     for name, sl in zip(names, slices):
         rows = [seq[i][2] for i in sl]
@@ -125,10 +131,10 @@ def summarize(args):
                               'factor': factor}
             gseq = gemm_sequence([(d, n, v) for d, (n, v) in vals.items()])
             # Under --pmc bench.py runs with the warmup/steps given on the command line.
-            psl, _ = phase_slices(len(names), args.pmc_warmup, args.pmc_steps)
-            exp = (args.pmc_warmup + args.pmc_steps) * len(names) + max(5, args.pmc_steps) * len(names)
+            psl, preps = phase_slices(len(names), args.pmc_steps, rot)
+            exp = (rot + args.pmc_warmup + args.pmc_steps) * len(names) + preps * len(names)
             if len(gseq) != exp:
-                sys.exit(f'{path}: expected {exp} GEMM dispatches, found {len(gseq)}')
+                sys.exit(f'{path}: expected {exp} library dispatches, found {len(gseq)}')
             for name, sl in zip(names, psl):
                 kib = sum(gseq[i][2] for i in sl) / len(sl)
                 traffic.setdefault(name, {})[counter] = kib * 1024.0 / factor
@@ -145,7 +151,7 @@ def summarize(args):
         gui = read_counters(args.mfma, 'GRBM_GUI_ACTIVE')
         bseq = gemm_sequence([(d, n, v) for d, (n, v) in busy.items()])
         gseq2 = gemm_sequence([(d, n, v) for d, (n, v) in gui.items()])
-        psl, _ = phase_slices(len(names), args.pmc_warmup, args.pmc_steps)
+        psl, _ = phase_slices(len(names), args.pmc_steps, rot)
         mfma = {}
         for name, sl, p in zip(names, psl, per):
             b = sum(bseq[i][2] for i in sl) / len(sl)
@@ -155,8 +161,9 @@ def summarize(args):
     lines = []
     lines.append(f"# {bench['config']['workload']}\n")
     lines.append('Kernel durations from `rocprofv3 --kernel-trace --stats`, per-launch timing phase of '
-                 'bench.py (back-to-back repetitions of one shape), next to the HIP-event average that '
-                 'bench.py measured in the same run.\n')
+                 f'bench.py (after a cache flush, {rot} back-to-back launches of one shape on rotating buffer '
+                 'sets, repeated), next to the HIP-event average per launch that bench.py measured in the '
+                 'same run.\n')
     lines.append('Commands (repository root on the GPU box; `OUT` = an output folder):\n')
     lines.append('```')
     for c in args.command or []:

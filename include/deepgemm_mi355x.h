@@ -178,6 +178,21 @@ int dg_plan_sf_transform(const dg_tensor* sf, int32_t mn, int32_t k,
                          int32_t num_groups, int32_t is_sfa,
                          int32_t disable_ue8m0_cast, int32_t* kind);
 
+/* ---------------------------------------------------------------- activation cast */
+
+/* Fused per-token FP8 cast of BF16 activations, for the GEMM's A operand: the
+ * reference's per_token_cast_to_fp8 (deep_gemm/utils/math.py:26-49, torch ops in
+ * the reference) in one HBM pass that writes the scales straight into the
+ * layout the caller's `sf` describes (K-major, or the MN-major TMA-aligned
+ * layout of get_mn_major_tma_aligned_tensor, which then needs no transpose).
+ *   x   bf16 [M, K], unit stride along K (K < 2^27)
+ *   q   e4m3 [M, K], unit stride along K
+ *   sf  f32 [M, ceil(K/gran_k)], any strides; or int32 [M, ceil(ceil(K/gran_k)/4)]
+ *       of packed UE8M0 exponents (needs use_ue8m0; groups past the last pack as 1.0)
+ *   gran_k 32, 64 or 128; use_ue8m0 rounds scales up to powers of two. */
+int dg_per_token_cast_to_fp8(const dg_tensor* x, const dg_tensor* q, const dg_tensor* sf,
+                             int32_t gran_k, int32_t use_ue8m0, void* stream);
+
 /* ---------------------------------------------------------------- knobs */
 
 /* Replace set_num_sms / get_num_sms (csrc/apis/config.hpp:15-20,

@@ -1,0 +1,113 @@
+"""HIP graph capture of the library's launches.
+
+The library allocates nothing and records no memset, so a call made while a
+stream captures is recorded as its kernels alone. Each test runs a call
+eagerly, captures the same call into a graph, and replays it several times with
+eager work (an overwrite of the outputs) and a synchronisation between
+replays; every replay must reproduce the eager bits.
+"""
+import numpy as np
+import pytest
+import torch
+
+import deep_gemm
+import generators as gen
+
+pytestmark = pytest.mark.gpu
+DEV = 'cuda'
+REPLAYS = 4
+
+
+def e4m3(x):
+    return gen.to_dev(x, torch.float8_e4m3fn)
+
+
+def f32(x):
+    return gen.to_dev(np.asarray(x, dtype=np.float32))
+
+
+def bits(t):
+    return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32) if t.element_size() == 4 \
+        else t.view(torch.uint8)
+
+
+def replay_matches_eager(run, out, written=None):
+    """run() writes `out` (the rows where `written` is true, else all of it);
+    compare graph replays of it with one eager call. Rows it does not write
+    must keep what the eager work between replays put there."""
+    run()
+    torch.cuda.synchronize()
+    sel = (lambda t: t[written]) if written is not None else (lambda t: t)
+    ref = bits(sel(out)).clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    for i in range(REPLAYS):
+        bits(out).fill_(0x5A + i)      # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(sel(out)), ref), f'replay {i} differs from the eager call'
+        if written is not None:
+            assert bool((bits(out[~written]) == 0x5A + i).all()), 'rows the call must not write were written'
+
+
+def test_graph_dense_bf16_and_accumulate():
+    print('graph dense m=520 n=768 k=1024', flush=True)
+    m, n, k = 520, 768, 1024
+    x = gen.dense_inputs(m, n, k, seed=21)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    replay_matches_eager(lambda: deep_gemm.fp8_gemm_nt(a, b, d), d)
+    c = torch.randn((m, n), generator=torch.Generator().manual_seed(3)).to(DEV)
+    d32 = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    replay_matches_eager(lambda: deep_gemm.fp8_gemm_nt(a, b, d32, c=c), d32)
+
+
+def test_graph_grouped_contiguous_and_masked():
+    print('graph contiguous g=4 / masked g=4', flush=True)
+    ms, aligned = gen.contiguous_sizes(4, 900, seed=5)
+    n, k = 512, 1024
+    x = gen.contiguous_inputs(ms, aligned, n, k, seed=22)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    idx = gen.to_dev(x['m_indices'])
+    d = torch.zeros((sum(aligned), n), dtype=torch.bfloat16, device=DEV)
+    # padding rows (m_indices == -1) are left untouched
+    replay_matches_eager(lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, idx), d, written=idx >= 0)
+
+    y = gen.masked_inputs(4, 256, n, k, seed=23)
+    a, b = (e4m3(y['qa']), f32(y['sfa'])), (e4m3(y['qb']), f32(y['sfb']))
+    mm = gen.to_dev(y['masked_m'])
+    dm = torch.zeros((4, 256, n), dtype=torch.bfloat16, device=DEV)
+    # rows >= masked_m are left untouched
+    valid = torch.arange(256, device=DEV)[None, :] < mm[:, None]
+    replay_matches_eager(lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, dm, mm, 128), dm, written=valid)
+
+
+def test_graph_fp8_fp4_packed():
+    print('graph fp8xfp4 m=256 n=512 k=1024', flush=True)
+    m, n, k = 256, 512, 1024
+    x = gen.fp8_fp4_inputs(m, n, k, seed=24)
+    sfa = deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(f32(x['sfa']))
+    sfb = deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(f32(x['sfb']))
+    a, b = (e4m3(x['qa']), sfa), (gen.to_dev(x['qb'], torch.int8), sfb)
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    replay_matches_eager(lambda: deep_gemm.fp8_fp4_gemm_nt(a, b, d, recipe_a=(1, 128), recipe_b=(1, 32)), d)
+
+
+def test_graph_cast():
+    print('graph per_token_cast m=300 k=1536', flush=True)
+    xb = torch.from_numpy(gen.randn_bf16((300, 1536), 25)).bfloat16().to(DEV)
+    q0, sf0 = deep_gemm.per_token_cast_to_fp8_mn_major(xb, use_ue8m0=False)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q, sf = deep_gemm.per_token_cast_to_fp8_mn_major(xb, use_ue8m0=False)
+    for i in range(REPLAYS):
+        q.view(torch.uint8).fill_(0x5A + i)
+        sf.fill_(float(i))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
+        assert torch.equal(sf.view(torch.int32), sf0.view(torch.int32))
