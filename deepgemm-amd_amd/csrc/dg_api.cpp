@@ -334,8 +334,9 @@ bool is_ue8m0_path(const Operands& o, const Recipe& r) {
     return gran_ok && (fp4 || packed || r.gran_k_a == 32 || r.gran_k_b == 32);
 }
 
+// expected_m: the masked layout's per-group row hint (tile choice only), else -1.
 void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int64_t n, int64_t k, int64_t groups,
-              int disable_ue8m0_cast, int zero_padding, hipStream_t stream) {
+              int disable_ue8m0_cast, int zero_padding, hipStream_t stream, int expected_m = -1) {
     const int align_m = g_mk_alignment.load();
     const bool grouped_b = kind != kNormal;
     const bool grouped_a = kind == kMasked;
@@ -374,11 +375,25 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.grid_limit = 256;
         try { args.grid_limit = num_sms_now(); } catch (const Error&) {}
         const int64_t m_rows = m;
-        const TileConfig t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
+        const int tv = g_tile_variant.load();
+        TileConfig t;
+        if (tv == 5) {   // forced: the masked weight-streaming kernel
+            if (kind != kMasked || !fp8_masked_stream_supported(args))
+                DG_UNSUPPORTED("tile override: the weight-streaming kernel runs the masked layout with K % 128 == 0");
+            t = {kMaskedStreamRows, g_tile_n.load(), 5};
+        } else if (tv == 0 && kind == kMasked && expected_m <= kMaskedStreamRows && fp8_masked_stream_supported(args)) {
+            // decode-sized groups: the weight-streaming kernel (one pass per group
+            // when masked_m <= 160; larger groups take more passes)
+            t = {kMaskedStreamRows, 32 * fp8_masked_stream_waves(n, groups, args.grid_limit), 5};
+        } else {
+            t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
+        }
         if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
-        if (t.variant >= 2)
+        if (t.variant == 5)
+            launch_fp8_gemm_masked_stream(args, t.block_n / 32, stream);
+        else if (t.variant >= 2)
             launch_fp8_gemm_1d2d_v2(kind, t, args, stream);
         else
             launch_fp8_gemm_1d2d(kind, t, args, stream);
@@ -532,7 +547,8 @@ void masked_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_
     const Recipe r = resolve_recipe(recipe, sfa, sfb);
     check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, g);
     check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, g);
-    run_gemm(kMasked, Operands{a, sfa, b, sfb, d, nullptr, masked_m_}, r, m, n, k, g, disable_ue8m0_cast, 0, stream);
+    run_gemm(kMasked, Operands{a, sfa, b, sfb, d, nullptr, masked_m_}, r, m, n, k, g, disable_ue8m0_cast, 0, stream,
+             expected_m);
 }
 
 // ---------------------------------------------------------------- SF layouts
@@ -771,6 +787,8 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
         }
         const bool ok = variant == 1   ? fp8_1d2d_tile_supported(block_m, block_n)
                         : variant == 2 ? fp8_1d2d_v2_tile_supported(block_m, block_n)
+                        : variant == 5 ? (block_m == kMaskedStreamRows && block_n % 32 == 0 && block_n >= 128 &&
+                                          block_n <= 256)
                                        : (variant == 4 && block_m == 256 && block_n == 256);
         if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;

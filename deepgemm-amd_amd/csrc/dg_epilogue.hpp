@@ -110,8 +110,11 @@ struct RowEpilogue {
                 const int m = row0 + p0 + r;
                 const int n = col0 + v0;
                 const int wr = p0 + r;   // wave-local row
-                const uint64_t sm = NMASK == 1 ? smask[0] : smask[(wr >> 6) & (NMASK - 1)];
-                const uint64_t zm = NMASK == 1 ? zmask[0] : zmask[(wr >> 6) & (NMASK - 1)];
+                // (wr < WM, so wr >> 6 < NMASK; the mask only helps the compiler)
+                constexpr bool POW2 = (NMASK & (NMASK - 1)) == 0;
+                const int mi = POW2 ? ((wr >> 6) & (NMASK - 1)) : (wr >> 6);
+                const uint64_t sm = NMASK == 1 ? smask[0] : smask[mi];
+                const uint64_t zm = NMASK == 1 ? zmask[0] : zmask[mi];
                 const bool store = (sm >> (wr & 63)) & 1, zero = (zm >> (wr & 63)) & 1;
                 float v[VPL];
                 const int byte = v0 * ES;

@@ -1,0 +1,317 @@
+// Weight-streaming kernel for the masked grouped FP32-scale FP8 GEMM (gfx950):
+// m_grouped_fp8_gemm_nt_masked at decode sizes, where each expert has a few
+// hundred rows at most and the launch is bound by reading B once from HBM.
+//
+// Arithmetic is the pipelined kernel's, bit for bit: per 128-wide K block two
+// v_mfma_f32_32x32x64_f8f6f4 into a fresh accumulator, then fin = fma(sa * sb,
+// acc, fin) (reference: deep_gemm/include/deep_gemm/impls/sm90_fp8_gemm_1d2d.cuh
+// :281-345), the same fragment K order, and the same row epilogue.
+//
+// What differs is the memory pipeline. One workgroup owns one expert and BN =
+// 32 * NW columns, and all of the expert's rows (up to 160 per pass):
+//  * wave w computes columns [32w, 32w + 32) for every 32-row tile below
+//    masked_m, so the whole workgroup shares one copy of A in LDS and each B
+//    byte is read from HBM once;
+//  * the pass is specialized on its number of 32-row tiles NRT (a switch on the
+//    device-side count): only those rows of A are loaded, the compute is
+//    straight-line code, and the A ring gets as many stages as fit;
+//  * A and B have separate LDS rings: 3 stages of B (the weight stream, loaded
+//    non-temporally) and S_A stages of A (3 or 4 by NRT; A rows come from L2
+//    after the expert's first workgroup). A(kb + S_A - 1) and B(kb + 2) are
+//    issued before K block kb computes, so two B stages are in flight while a
+//    block computes; B(0) and B(1) are issued before masked_m is even read;
+//  * SFB comes in by scalar loads one K block ahead (no vector-memory count);
+//  * all stage loads are global_load_lds_dwordx4 / _dword with the same
+//    per-wave count, so one s_waitcnt vmcnt immediate serves every wave;
+//  * workgroups of one expert run on one XCD (logical tiles are expert-major
+//    and mapped to XCDs in contiguous ranges), so A rows reach HBM once per XCD.
+// Requirements (checked by the host): K a multiple of 128 with at most 128 K
+// blocks, BF16 D without C, 16-byte aligned A/B/D rows.
+#include <hip/hip_runtime.h>
+
+#include "dg_internal.hpp"
+#include "dg_kernel_common.hpp"
+#include "dg_epilogue.hpp"
+#include "dg_lds_dma.hpp"
+
+namespace dgm {
+namespace {
+
+using namespace dev;
+
+constexpr int kBK = 128;
+constexpr int kMR = kMaskedStreamRows;    // A rows per pass: up to 5 MFMA row tiles of 32
+static_assert(kMR == 160, "five row tiles");
+constexpr int kMaxKB = 128;
+constexpr int kLds = 163840;              // the stage rings (and the epilogue's staging): all of the CU's LDS
+
+// LDS chunk phase of a row, as in the pipelined kernel: 16 consecutive rows at
+// one logical 16-byte chunk land on distinct banks.
+__device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
+typedef const __attribute__((address_space(4))) float cfloat;
+
+// B (the weight stream) stage loads, non-temporal so they do not push the
+// expert's A rows out of L2: B ring slot `st` at LDS offset 0.
+template <int NW>
+struct StreamShape {
+    static constexpr int BN = NW * 32;
+    static constexpr int B_STAGE = BN * kBK;
+    static constexpr int B_RING = 3 * B_STAGE;
+    static constexpr int LB = BN / (8 * NW);   // B loads per stage and wave (= 4)
+
+    // Column (LDS row) 8 * (i * NW + wave) + rs of load i, clamped to the last
+    // column that exists; the 16-byte chunk is swizzled by the LDS row.
+    __device__ static void offsets(uint32_t (&voff)[LB], int wave, int rs, int pc, int b_rows, int64_t ldb) {
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const int row = (i * NW + wave) * 8 + rs;
+            voff[i] = (uint32_t)min(row, b_rows - 1) * (uint32_t)ldb + ((pc ^ swz_g(row)) << 4);
+        }
+    }
+    __device__ static void issue(const uint8_t* b_t, const uint32_t (&voff)[LB], int num_kb, int kb, int st,
+                                 int wave, uint32_t smem_lds) {
+        kb = min(kb, num_kb - 1);   // past the end: reload the last block into the free slot
+        const uint8_t* base = b_t + (int64_t)kb * kBK;
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const uint32_t lds = smem_lds + st * B_STAGE + (i * NW + wave) * 1024;
+            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds), "v"(voff[i]),
+                         "s"(base)
+                         : "memory", "m0");
+        }
+    }
+};
+
+// One pass over rows [r0, r0 + 32 * NRT) of the expert (a_rows of them valid).
+// b_primed: B(0) and B(1) are already in flight (issued by the caller).
+template <int NW, int NRT>
+__device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem, const uint8_t* b_t,
+                                            const uint32_t (&voff_b)[StreamShape<NW>::LB], bool b_primed, int g,
+                                            int n0, int r0, int a_rows, int m_g, int wave, int lane) {
+    using S = StreamShape<NW>;
+    constexpr int ROWS = NRT * 32;
+    constexpr int A_SEGS = ROWS / 8;                        // 1 KB (8-row) wave loads of A per stage
+    constexpr int A_INSTR = (A_SEGS + NW - 1) / NW;         // per wave; surplus loads repeat the last segment
+    constexpr int SA_SEGS = (ROWS + 63) / 64;               // 256 B SFA loads per stage (one per wave, clamped)
+    constexpr int A_STAGE = ROWS * kBK + SA_SEGS * 256;
+    constexpr int SA = (kLds - S::B_RING) / A_STAGE > 4 ? 4 : (kLds - S::B_RING) / A_STAGE;
+    constexpr int LA = A_INSTR + 1;
+    constexpr int LB = S::LB;
+    // At the end of block kb, A(kb + 1) and B(kb + 1) must be complete; the loads
+    // issued after the later of them are B(kb + 2) (two A stages) or all of
+    // block kb's (more).
+    constexpr int W = SA == 2 ? LB : LA + LB;
+    static_assert(SA >= 2, "two A stages fit");
+    static_assert(LA + LB < 64, "vmcnt range");
+
+    const int num_kb = p.k / kBK;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int rs = lane >> 3, pc = lane & 7;
+    const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    const uint32_t a_ring = smem_lds + S::B_RING;
+
+    // Fragment reads: lane (lrow, lhalf) takes row r0 + lrow, logical chunks
+    // 4ks + 2lhalf and 4ks + 2lhalf + 1 (K bytes [64ks + 32lhalf, +32)).
+    const int gl = swz_g(lrow);
+    uint32_t frag_off[2][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) frag_off[ks][h] = lrow * 128 + (((4 * ks + 2 * lhalf + h) ^ gl) << 4);
+    auto frag = [&](const uint8_t* tile, int rr, int ks) {
+        const uint8_t* slab = tile + rr * 128;
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(slab + frag_off[ks][0]);
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(slab + frag_off[ks][1]);
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    const uint8_t* __restrict__ a_p = p.a + (int64_t)g * p.a_gs + (int64_t)r0 * p.lda;
+    const float* __restrict__ sa_p = p.sfa + (int64_t)g * p.sfa_gs + (int64_t)r0 * p.sfa_sm;
+
+    // Per-lane offsets of the A stage loads: rows past a_rows repeat the last
+    // valid one, whose outputs are never stored.
+    uint32_t voff_a[A_INSTR];
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {
+        const int row = min(i * NW + wave, A_SEGS - 1) * 8 + rs;
+        voff_a[i] = (uint32_t)min(row, a_rows - 1) * (uint32_t)p.lda + ((pc ^ swz_g(row)) << 4);
+    }
+    const int sa_seg = min(wave, SA_SEGS - 1);
+    const uint32_t voff_sa = (uint32_t)(min(sa_seg * 64 + lane, a_rows - 1) * p.sfa_sm) * 4u;
+    auto issue_a = [&](int kb, int st) {
+        kb = min(kb, num_kb - 1);   // past the end: reload the last block into the free slot
+        const uint32_t lds = a_ring + st * A_STAGE;
+        const uint8_t* base = a_p + (int64_t)kb * kBK;
+#pragma unroll
+        for (int i = 0; i < A_INSTR; ++i) dma16_saddr(base, voff_a[i], lds + min(i * NW + wave, A_SEGS - 1) * 1024);
+        dma4_saddr(reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk), voff_sa,
+                   lds + ROWS * kBK + sa_seg * 256);
+    };
+    auto issue_b = [&](int kb, int st) { S::issue(b_t, voff_b, num_kb, kb, st, wave, smem_lds); };
+    // The wave's SFB column (its 32 columns lie in one 128-row group), read with
+    // scalar loads one K block ahead.
+    cfloat* sfb_w = (cfloat*)(p.sfb + (int64_t)g * p.sfb_gs +
+                              (int64_t)min((n0 + wave * 32) >> 7, (p.n - 1) >> 7) * p.sfb_sn);
+    float sb_next = sfb_w[0];
+
+    f32x16 fin[NRT][1];
+#pragma unroll
+    for (int i = 0; i < NRT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) fin[i][0][e] = 0.f;
+
+    // Prologue B(0), B(1) (unless in flight already), A(0 .. SA-2); wait until
+    // only A(1 .. SA-2) may be in flight.
+    if (!b_primed) {
+        issue_b(0, 0);
+        issue_b(1, 1);
+    }
+#pragma unroll
+    for (int s = 0; s < SA - 1; ++s) issue_a(s, s);
+    wait_vmcnt_barrier<(SA - 2) * LA>();
+    for (int kb = 0; kb < num_kb; ++kb) {
+        // The slots refilled here held K block kb - 1, which every wave finished
+        // before the last barrier.
+        issue_a(kb + SA - 1, (kb + SA - 1) % SA);
+        issue_b(kb + 2, (kb + 2) % 3);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* a_tile = smem + S::B_RING + (kb % SA) * A_STAGE;
+        const uint8_t* b_tile = smem + (kb % 3) * S::B_STAGE;
+        const i32x8 ob0 = frag(b_tile, wave * 32, 0), ob1 = frag(b_tile, wave * 32, 1);
+        const float sb = sb_next;
+        sb_next = sfb_w[(int64_t)min(kb + 1, num_kb - 1) * p.sfb_sk];
+        // Row tile rt + 1's A fragment is read while rt's MFMA pair runs, and rt's
+        // pair is issued before rt - 1 is promoted, so LDS reads and FMAs overlap
+        // the matrix core. (The scheduling barriers keep the compiler from
+        // hoisting every row tile's reads, which would hold them all in registers.)
+        f32x16 acc[2];
+        float scl[2];
+        i32x8 oa[2][2];
+        oa[0][0] = frag(a_tile, 0, 0);
+        oa[0][1] = frag(a_tile, 0, 1);
+#pragma unroll
+        for (int rt = 0; rt <= NRT; ++rt) {
+            if (rt < NRT) {
+                if (rt + 1 < NRT) {
+                    oa[(rt + 1) & 1][0] = frag(a_tile, (rt + 1) * 32, 0);
+                    oa[(rt + 1) & 1][1] = frag(a_tile, (rt + 1) * 32, 1);
+                }
+                const float sa = *reinterpret_cast<const float*>(a_tile + ROWS * kBK + (rt * 32 + lrow) * 4);
+                const f32x16 c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ob0, oa[rt & 1][0], f32x16{}, 0, 0,
+                                                                                 0, 0, 0, 0);
+                acc[rt & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ob1, oa[rt & 1][1], c, 0, 0, 0, 0, 0,
+                                                                              0);
+                scl[rt & 1] = sa * sb;
+            }
+            if (rt >= 1) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    fin[rt - 1][0][e] = __builtin_fmaf(scl[(rt - 1) & 1], acc[(rt - 1) & 1][e], fin[rt - 1][0][e]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_barrier<W>();
+    }
+    // No stage load may still be writing LDS when the epilogue reuses it.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    Tile t{};
+    t.g = g, t.expert = g, t.m0 = r0, t.n0 = n0, t.row_end = m_g, t.active = 1;
+    using Epi = RowEpilogue<kMasked, 0, 0, NRT, 1>;
+    constexpr int REGION = kLds / NW / 16 * 16;
+    Epi::template run<Epi::rows_per_pass(REGION)>(fin, smem + wave * REGION, lane, t, p.m, p.layout, r0,
+                                                  n0 + wave * 32, p.n, r0, r0 + ROWS, p.d, nullptr, p.ldd, 0,
+                                                  (int64_t)g * p.d_gs);
+}
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64, 1)
+fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
+    static_assert(NW >= 4 && NW <= 8, "4 to 8 waves");
+    using S = StreamShape<NW>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lt = xcd_remap(blockIdx.x, gridDim.x);
+    const int g = lt / num_n_tiles;
+    const int n0 = (lt - g * num_n_tiles) * S::BN;
+    const int num_kb = p.k / kBK;
+
+    // The first two B stages do not depend on masked_m: start them before it is read.
+    const uint8_t* __restrict__ b_t = p.b + (int64_t)g * p.b_gs + (int64_t)n0 * p.ldb;
+    uint32_t voff_b[S::LB];
+    S::offsets(voff_b, wave, lane >> 3, lane & 7, min(S::BN, p.n - n0), p.ldb);
+    const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    S::issue(b_t, voff_b, num_kb, 0, 0, wave, smem_lds);
+    S::issue(b_t, voff_b, num_kb, 1, 1, wave, smem_lds);
+
+    const int m_g = min(((const __attribute__((address_space(4))) int32_t*)p.layout)[g], p.m);   // masked_m
+    if (m_g <= 0) {   // uniform over the workgroup; no stage load may outlive it
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
+    for (int r0 = 0; r0 < m_g; r0 += kMR) {
+        if (r0 > 0) __syncthreads();   // the previous pass's epilogue is done with the LDS
+        const int a_rows = min(kMR, m_g - r0);
+        const int nrt = __builtin_amdgcn_readfirstlane((a_rows + 31) >> 5);
+        const bool primed = r0 == 0;
+        switch (nrt) {
+            case 1: masked_pass<NW, 1>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 2: masked_pass<NW, 2>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 3: masked_pass<NW, 3>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 4: masked_pass<NW, 4>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            default: masked_pass<NW, 5>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+        }
+    }
+}
+
+template <int NW>
+void launch_nw(const Fp8GemmArgs& a, hipStream_t stream) {
+    constexpr int BN = NW * 32;
+    const int num_n_tiles = (a.n + BN - 1) / BN;
+    const int64_t grid = (int64_t)num_n_tiles * a.num_groups;
+    if (grid == 0) return;
+    DG_CHECK(grid < (int64_t)1 << 31);
+    hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
+                       num_n_tiles);
+    DG_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+bool fp8_masked_stream_supported(const Fp8GemmArgs& a) {
+    return a.k > 0 && a.k % kBK == 0 && a.k / kBK <= kMaxKB && !a.out_f32 && a.c == nullptr && a.n > 0;
+}
+
+int fp8_masked_stream_waves(int64_t n, int64_t groups, int cus) {
+    // Each workgroup streams BN * K bytes of B; one resident per CU. Cost =
+    // rounds of workgroups x work of one, smallest wins (ties: wider tiles).
+    int best_nw = 8;
+    double best = 1e300;
+    for (int nw = 8; nw >= 4; --nw) {
+        const int64_t bn = 32 * nw;
+        const int64_t tiles = (n + bn - 1) / bn * groups;
+        const double cost = (double)((tiles + cus - 1) / cus) * (double)bn;
+        if (cost < best - 1e-9) best = cost, best_nw = nw;
+    }
+    return best_nw;
+}
+
+void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& a, int waves, hipStream_t stream) {
+    DG_CHECK(fp8_masked_stream_supported(a));
+    switch (waves) {
+        case 4: launch_nw<4>(a, stream); break;
+        case 5: launch_nw<5>(a, stream); break;
+        case 6: launch_nw<6>(a, stream); break;
+        case 7: launch_nw<7>(a, stream); break;
+        case 8: launch_nw<8>(a, stream); break;
+        default: DG_UNSUPPORTED("masked streaming kernel: 4 to 8 waves (block_n 128 to 256 in steps of 32)");
+    }
+}
+
+}  // namespace dgm

@@ -81,7 +81,9 @@ struct Fp8GemmArgs {
 struct TileConfig {
     int block_m;
     int block_n;
-    int variant = 1;   // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined, 4 = 2 persistent
+    // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined, 4 = 2 persistent,
+    // 5 = masked weight-streaming (block_m 160 rows per pass, block_n = 32 x waves)
+    int variant = 1;
 };
 
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
@@ -96,6 +98,14 @@ bool fp8_1d2d_tile_supported(int block_m, int block_n);
 void launch_fp8_gemm_1d2d_v2(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args,
                              hipStream_t stream);
 bool fp8_1d2d_v2_tile_supported(int block_m, int block_n);
+
+// The masked weight-streaming kernel (dg_gemm_fp8_masked.hip): K a multiple of
+// 128 (at most 128 blocks), BF16 D without C. `waves` = block_n / 32, 4 to 8.
+// A pass covers kMaskedStreamRows rows of a group.
+constexpr int kMaskedStreamRows = 160;
+bool fp8_masked_stream_supported(const Fp8GemmArgs& args);
+int fp8_masked_stream_waves(int64_t n, int64_t groups, int cus);
+void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& args, int waves, hipStream_t stream);
 
 // Arguments of the UE8M0 block-scaled kernel (A e4m3 or e2m1, B e4m3 or e2m1,
 // scales applied inside the scaled MFMA).

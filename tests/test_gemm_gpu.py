@@ -310,6 +310,36 @@ def test_masked_edge_counts():
             assert not bool((d[i, :r].view(torch.int16) == SENTINEL).any())
 
 
+@pytest.mark.parametrize('bn,mn_major', [(128, False), (160, True), (192, False), (224, True), (256, False),
+                                         (256, True)])
+def test_masked_stream_equals_pipelined(bn, mn_major):
+    """The weight-streaming masked kernel (variant 5) is bitwise equal to the
+    pipelined 256 x 256 kernel: masked_m of 0, 1, one pass (97, 160), two passes
+    (161, 300), N not a multiple of block_n, K-major and MN-major SFA."""
+    g, max_m, n, k = 6, 320, 480, 1024
+    x = gen.masked_inputs(g, max_m, n, k, seed=bn + int(mn_major))
+    x['masked_m'][:] = [0, 1, 160, 161, 300, 97]
+    print(f'masked stream block_n={bn} mn_major={mn_major} masked_m={x["masked_m"].tolist()}', flush=True)
+    sfa = f32(x['sfa'])
+    if mn_major:
+        sfa = deep_gemm.get_mn_major_tma_aligned_tensor(sfa)
+    a, b = (e4m3(x['qa']), sfa), (e4m3(x['qb']), f32(x['sfb']))
+    mm = gen.to_dev(x['masked_m'])
+    outs = {}
+    for v, (bm_, bn_) in [(2, (256, 256)), (5, (160, bn))]:
+        d = sentinel_bf16((g, max_m, n))
+        deep_gemm.set_tile_override(bm_, bn_, variant=v)
+        try:
+            deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, expected_m=128)
+            cfg = deep_gemm.get_last_config()
+        finally:
+            deep_gemm.set_tile_override(0, 0)
+        torch.cuda.synchronize()
+        assert f' v{v} ' in cfg and f'block_n={bn_}' in cfg, cfg
+        outs[v] = d
+    assert torch.equal(outs[2].view(torch.int16), outs[5].view(torch.int16))
+
+
 # ------------------------------------------------- persistent workgroups (variant 4)
 
 def _with_variant(v, fn):
