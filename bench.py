@@ -15,7 +15,8 @@ overhead out of the timed region; --eager launches from Python instead.
 Other workloads (`--workload`): dense_acc (FP32 C += A.B^T), contiguous
 (config 3, 8 experts, 32768 tokens), masked (config 4, 16 experts, max_m 256),
 fp8fp4 (config 5), cast (the fused per-token FP8 activation cast that produces
-A and its MN-major SFA for these GEMMs; HBM-bound, reported in GB/s).
+A and its MN-major SFA for these GEMMs; HBM-bound, reported in GB/s), kgrouped
+(k_grouped_fp8_gemm_nt_contiguous, the 1D1D weight-gradient GEMM).
 
 Prints one JSON line. `roofline` is computed from per-launch durations measured
 live with HIP events on the launch stream; `cpu_baseline` times the oracle/
@@ -40,7 +41,7 @@ DENSE_NK = [(2112, 7168), (24576, 1536), (7168, 16384), (4096, 7168), (7168, 204
 PROFILE_NAMES = {'dense': 'fp8_gemm_nt_dense_m4096', 'dense_acc': 'fp8_gemm_nt_dense_acc_m4096',
                  'contiguous': 'm_grouped_fp8_gemm_nt_contiguous_e8_t32768',
                  'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096',
-                 'cast': 'per_token_cast_to_fp8_bf16'}
+                 'cast': 'per_token_cast_to_fp8_bf16', 'kgrouped': 'k_grouped_fp8_gemm_nt_e8_m4096_n7168'}
 
 
 def parse():
@@ -49,7 +50,7 @@ def parse():
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--workload', default='dense',
-                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast'])
+                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--rotate', type=int, default=8, help='rotating buffer sets per launch')
     ap.add_argument('--eager', action='store_true', help='launch from Python instead of replaying HIP graphs')
@@ -226,6 +227,39 @@ def make_fp8fp4():
     return [Launch('m4096_n7168_k7168', mk, 2 * m * n * k, nbytes)], cfg, 'mfma'
 
 
+def make_kgrouped():
+    """k_grouped_fp8_gemm_nt_contiguous, the reference's EP32 weight-gradient case
+    (tests/generators.py:229-262): 8 groups, M = 4096, N = 7168, K_g ~ 4096 x U[0.7, 1.3]
+    aligned to 128, FP32 D += A_g.B_g^T in place."""
+    import numpy as np
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    rng = np.random.default_rng(0)
+    g, m, n = 8, 4096, 7168
+    ks = [int((4096 * rng.uniform(0.7, 1.3) + 127) // 128 * 128) for _ in range(g)]
+    sum_k = sum(ks)
+    torch.manual_seed(0)
+    qa, sa, qb, sb = [], [], [], []
+    for k in ks:   # per-group 1 x 128 casts of randn rows, on the device
+        q, sf = deep_gemm.per_token_cast_to_fp8(torch.randn((m, k), device=dev, dtype=torch.bfloat16), False)
+        qa.append(q.view(torch.uint8).reshape(-1)), sa.append(sf)
+        q, sf = deep_gemm.per_token_cast_to_fp8(torch.randn((n, k), device=dev, dtype=torch.bfloat16), False)
+        qb.append(q.view(torch.uint8).reshape(-1)), sb.append(sf)
+    qa, qb = torch.cat(qa).view(torch.float8_e4m3fn), torch.cat(qb).view(torch.float8_e4m3fn)
+    sfa, sfb = torch.cat(sa, dim=1), torch.cat(sb, dim=1)
+    d0 = torch.randn((g, m, n), device=dev) * 32
+    layout = torch.tensor(ks, dtype=torch.int32, device=dev)
+
+    def mk():
+        a2, b2, d2 = _twin((qa, sfa)), _twin((qb, sfb)), _twin(d0)
+        return lambda: deep_gemm.k_grouped_fp8_gemm_nt_contiguous(a2, b2, d2, ks, layout, d2)
+    nbytes = sum_k * (m + n) + 4 * (m + n) * (sum_k // 128) + 8 * g * m * n
+    cfg = {'workload': 'k_grouped_fp8_gemm_nt_contiguous 8 groups M=4096 N=7168 K_g~4096 (1D1D, FP32 D += )',
+           'ks': ks}
+    return [Launch(f'g{g}_m{m}_n{n}_sumk{sum_k}', mk, 2 * m * n * sum_k, nbytes)], cfg, 'mfma'
+
+
 CAST_MK = [(4096, 7168), (4096, 16384), (4096, 1536), (32768, 7168)]
 
 
@@ -312,7 +346,8 @@ def main():
     import deep_gemm
     torch.cuda.set_device(0)
     makers = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
-              'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast}
+              'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast,
+              'kgrouped': make_kgrouped}
     if args.calibrate_copy_mib > 0:
         x = torch.randn(args.calibrate_copy_mib * 1024 * 256, device='cuda:0')
         y = torch.empty_like(x)

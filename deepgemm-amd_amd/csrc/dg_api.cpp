@@ -243,6 +243,7 @@ const char* kind_name(GemmKind k) {
         case kContiguous: return "m_grouped_contiguous";
         case kMasked: return "m_grouped_masked";
         case kPsum: return "m_grouped_contiguous_psum";
+        case kKGrouped: return "k_grouped_contiguous";
     }
     return "?";
 }
@@ -324,6 +325,28 @@ bool is_1d2d(const Operands& o, const Recipe& r) {
     return o.a.dtype() == DG_E4M3 && o.b.dtype() == DG_E4M3 && o.sfa.dtype() == DG_F32 &&
            o.sfb.dtype() == DG_F32 && r.gran_mn_a == 1 && r.gran_k_a == 128 && r.gran_mn_b == 128 &&
            r.gran_k_b == 128;
+}
+
+// FP32 SF recipe of the reference's SM90 "1D1D" kernel (weight gradients):
+// A and B both 1 x 128 per row, both e4m3.
+bool is_1d1d(const Operands& o, const Recipe& r) {
+    return o.a.dtype() == DG_E4M3 && o.b.dtype() == DG_E4M3 && o.sfa.dtype() == DG_F32 &&
+           o.sfb.dtype() == DG_F32 && r.gran_mn_a == 1 && r.gran_k_a == 128 && r.gran_mn_b == 1 &&
+           r.gran_k_b == 128;
+}
+
+// Waves (block_n / 32) of the 1D1D kernel: whole rounds of one workgroup per
+// CU, weighted by the measured per-CU throughput of each width.
+int fp8_1d1d_waves(int64_t m, int64_t n, int64_t groups, int cus) {
+    static const struct { int nw; double eff; } cands[] = {{8, 1.0}, {6, 0.9}, {4, 0.7}};
+    int best_nw = 8;
+    double best = 1e300;
+    for (const auto& c : cands) {
+        const int64_t tiles = ceil_div(m, (int64_t)128) * ceil_div(n, (int64_t)(32 * c.nw)) * groups;
+        const double cost = (double)ceil_div(tiles, (int64_t)cus) * 32 * c.nw / c.eff;
+        if (cost < best - 1e-9) best = cost, best_nw = c.nw;
+    }
+    return best_nw;
 }
 
 bool is_ue8m0_path(const Operands& o, const Recipe& r) {
@@ -458,8 +481,36 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         return;
     }
 
-    if (o.sfa.dtype() == DG_F32 && o.sfb.dtype() == DG_F32 && r.gran_mn_b == 1)
-        DG_UNSUPPORTED("FP32-scale 1D1D recipe (gran_n == 1, reference sm90_fp8_gemm_1d1d) is not provided");
+    if (is_1d1d(o, r)) {
+        // csrc/jit_kernels/impls/sm90_fp8_gemm_1d1d.hpp:91: FP32 D, accumulating into C
+        DG_CHECK(o.c != nullptr && o.d.dtype() == DG_F32);
+        if (kind != kNormal) DG_UNSUPPORTED("the 1D1D recipe runs the dense and K-grouped GEMMs only");
+        if (k % 128 != 0) DG_UNSUPPORTED("the 1D1D recipe needs K to be a multiple of 128 here");
+        check_vector_alignment(o.a, "a");
+        check_vector_alignment(o.b, "b");
+        check_vector_alignment(o.d, "d");
+        check_vector_alignment(view(o.c, "c"), "c");
+        const View cv = view(o.c, "c");
+        Fp8GemmArgs args{};
+        args.a = static_cast<const uint8_t*>(o.a.data());
+        args.b = static_cast<const uint8_t*>(o.b.data());
+        args.sfa = static_cast<const float*>(o.sfa.data());
+        args.sfb = static_cast<const float*>(o.sfb.data());
+        args.d = const_cast<void*>(o.d.data());
+        args.c = cv.data();
+        args.m = (int32_t)m, args.n = (int32_t)n, args.k = (int32_t)k;
+        args.num_groups = 1;
+        args.out_f32 = 1;
+        args.lda = o.a.stride(-2), args.ldb = o.b.stride(-2), args.ldd = o.d.stride(-2), args.ldc = cv.stride(-2);
+        args.sfa_sm = o.sfa.stride(-2), args.sfa_sk = o.sfa.stride(-1);
+        args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
+        int cus = 256;
+        try { cus = num_sms_now(); } catch (const Error&) {}
+        const int waves = fp8_1d1d_waves(m, n, 1, cus);
+        record_config("fp8_gemm_1d1d", kind, TileConfig{128, 32 * waves, 6}, m, n, k, 1);
+        launch_fp8_gemm_1d1d(false, waves, args, stream);
+        return;
+    }
     DG_UNSUPPORTED("Unsupported architecture or scaling factor types");
 }
 
@@ -668,6 +719,91 @@ void cast_impl(const dg_tensor* x_, const dg_tensor* q_, const dg_tensor* sf_, i
     t_last_config = buf;
 }
 
+// csrc/apis/gemm.hpp:369-425 (k_grouped_fp8_gemm_nt_contiguous), with
+// check_k_grouped_args (:55-76) and early_return (:17-53).
+void k_grouped_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
+                    const dg_tensor* d_, const int32_t* ks, int32_t num_ks, const dg_tensor* layout_,
+                    const dg_tensor* c, const int32_t* recipe, int32_t use_psum_layout, hipStream_t stream) {
+    const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
+               d = view(d_, "d"), gl = view(layout_, "grouped_layout");
+    const int r0 = recipe ? recipe[0] : 1, r1 = recipe ? recipe[1] : 1, r2 = recipe ? recipe[2] : 128;
+    DG_CHECK(r0 == 1 && r1 == 1 && r2 == 128);   // recipe == std::make_tuple(1, 1, 128)
+    DG_CHECK(!use_psum_layout && ks != nullptr && num_ks > 0);
+    check_shape(d, 3);
+    const int64_t g = d.size(0), m = d.size(1), n = d.size(2);
+    auto numel = [](const View& t) {
+        int64_t e = 1;
+        for (int i = 0; i < t.dim(); ++i) e *= t.size(i);
+        return e;
+    };
+    auto contiguous = [](const View& t) {
+        int64_t want = 1;
+        for (int i = t.dim() - 1; i >= 0; --i) {
+            if (t.size(i) != 1 && t.stride(i) != want) return false;
+            want *= t.size(i);
+        }
+        return true;
+    };
+    DG_CHECK(contiguous(gl));
+    DG_CHECK(gl.dtype() == DG_I32);
+    DG_CHECK(numel(gl) == g);
+    DG_CHECK(gl.on_device());
+    DG_CHECK((int64_t)num_ks == g);
+    int64_t sum_k = 0;
+    for (int32_t i = 0; i < num_ks; ++i) {
+        DG_CHECK(ks[i] >= 0 && ks[i] % 128 == 0);
+        sum_k += ks[i];
+    }
+    DG_CHECK(numel(a) == sum_k * m);
+    DG_CHECK(numel(b) == sum_k * n);
+    DG_CHECK(contiguous(a));
+    DG_CHECK(contiguous(b));
+    DG_CHECK(contiguous(d));
+    DG_CHECK(c != nullptr && contiguous(view(c, "c")));
+    DG_CHECK(a.dtype() == DG_E4M3 && b.dtype() == DG_E4M3);
+    DG_CHECK(a.on_device() && b.on_device());
+    // csrc/jit_kernels/impls/sm90_fp8_gemm_1d1d.hpp:153: FP32 D, accumulating into C
+    DG_CHECK(d.dtype() == DG_F32);
+    const View cv = view(c, "c");
+    DG_CHECK(cv.dtype() == DG_F32 && cv.on_device() && cv.dim() == 3);
+    for (int i = 0; i < 3; ++i) DG_CHECK(cv.size(i) == d.size(i));
+    if (m == 0 || n == 0) return;
+    if (sum_k == 0) {   // D = C
+        if (cv.data() != d.data())
+            launch_fill_or_copy(const_cast<void*>(d.data()), cv.data(), (int)m, (int)n, (int)g, n, m * n, n, m * n,
+                                4, stream);
+        return;
+    }
+    // SF: [M, sum_k / 128] and [N, sum_k / 128], FP32, any strides (the kernel
+    // reads them in place; the reference makes them MN-major TMA-aligned first)
+    DG_CHECK(sfa.dim() == 2 && sfb.dim() == 2 && sfa.dtype() == DG_F32 && sfb.dtype() == DG_F32);
+    DG_CHECK(sfa.on_device() && sfb.on_device());
+    DG_CHECK(sfa.size(0) == m && sfa.size(1) == sum_k / 128);
+    DG_CHECK(sfb.size(0) == n && sfb.size(1) == sum_k / 128);
+    check_vector_alignment(d, "d");
+    check_vector_alignment(cv, "c");
+    DG_CHECK(reinterpret_cast<uintptr_t>(a.data()) % 16 == 0 && reinterpret_cast<uintptr_t>(b.data()) % 16 == 0);
+    Fp8GemmArgs args{};
+    args.a = static_cast<const uint8_t*>(a.data());
+    args.b = static_cast<const uint8_t*>(b.data());
+    args.sfa = static_cast<const float*>(sfa.data());
+    args.sfb = static_cast<const float*>(sfb.data());
+    args.d = const_cast<void*>(d.data());
+    args.c = cv.data();
+    args.layout = static_cast<const int32_t*>(gl.data());
+    args.m = (int32_t)m, args.n = (int32_t)n, args.k = 0;
+    args.num_groups = (int32_t)g;
+    args.out_f32 = 1;
+    args.ldd = n, args.ldc = n, args.d_gs = m * n, args.c_gs = m * n;
+    args.sfa_sm = sfa.stride(0), args.sfa_sk = sfa.stride(1);
+    args.sfb_sn = sfb.stride(0), args.sfb_sk = sfb.stride(1);
+    int cus = 256;
+    try { cus = num_sms_now(); } catch (const Error&) {}
+    const int waves = fp8_1d1d_waves(m, n, g, cus);
+    record_config("fp8_gemm_1d1d", kKGrouped, TileConfig{128, 32 * waves, 6}, m, n, sum_k, g);
+    launch_fp8_gemm_1d1d(true, waves, args, stream);
+}
+
 }  // namespace
 }  // namespace dgm
 
@@ -708,6 +844,27 @@ int dg_m_grouped_fp8_fp4_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor*
         contiguous_impl(a, sfa, b, sfb, d, grouped_layout, recipe, disable_ue8m0_cast, use_psum_layout,
                         ensure_zero_padding, expected_m_for_psum_layout, static_cast<hipStream_t>(stream));
     });
+}
+
+int dg_k_grouped_fp8_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
+                                        const dg_tensor* sfb, const dg_tensor* d, const int32_t* ks_cpu,
+                                        int32_t num_ks, const dg_tensor* grouped_layout, const dg_tensor* c,
+                                        const int32_t* recipe, int32_t use_psum_layout, void* stream) {
+    return guarded([&] {
+        k_grouped_impl(a, sfa, b, sfb, d, ks_cpu, num_ks, grouped_layout, c, recipe, use_psum_layout,
+                       static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_k_grouped_fp8_gemm_tn_contiguous(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
+                                        const dg_tensor* sfb, const dg_tensor* d, const int32_t* ks_cpu,
+                                        int32_t num_ks, const dg_tensor* grouped_layout, const dg_tensor* c,
+                                        const int32_t* recipe, int32_t use_psum_layout, void* stream) {
+    (void)a, (void)sfa, (void)b, (void)sfb, (void)d, (void)ks_cpu, (void)num_ks, (void)grouped_layout, (void)c;
+    (void)recipe, (void)use_psum_layout, (void)stream;
+    // The reference runs the MN-major (TN) form only with its SM100 kernel
+    // (csrc/apis/gemm.hpp:360-367); like its SM90 build, this one does not.
+    return guarded([&] { DG_UNSUPPORTED("Unsupported architecture: k_grouped_fp8_gemm_tn_contiguous"); });
 }
 
 int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,

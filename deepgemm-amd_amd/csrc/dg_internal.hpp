@@ -54,6 +54,7 @@ enum GemmKind : int {
     kContiguous = 1,   // m_indices [M]: expert of block = max(0, m_indices[block start])
     kMasked = 2,       // masked_m [G]: A/D are [G, max_m, *]
     kPsum = 3,         // psum ends [G]: group i rows [align(end[i-1]), end[i])
+    kKGrouped = 4,     // K sizes [G]: group i multiplies the K-slices of A and B into D[i]
 };
 
 // Arguments of the FP32-scale ("1D2D": 1x128 A scales, 128x128 B scales) kernel.
@@ -82,7 +83,8 @@ struct TileConfig {
     int block_m;
     int block_n;
     // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined, 4 = 2 persistent,
-    // 5 = masked weight-streaming (block_m 160 rows per pass, block_n = 32 x waves)
+    // 5 = masked weight-streaming (block_m 160 rows per pass, block_n = 32 x waves),
+    // 6 = 1D1D (block_m 128, block_n = 32 x waves)
     int variant = 1;
 };
 
@@ -106,6 +108,10 @@ constexpr int kMaskedStreamRows = 160;
 bool fp8_masked_stream_supported(const Fp8GemmArgs& args);
 int fp8_masked_stream_waves(int64_t n, int64_t groups, int cus);
 void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& args, int waves, hipStream_t stream);
+
+// The 1D1D (per-row B scales) kernel, dense or K-grouped (dg_gemm_fp8_1d1d.hip):
+// FP32 D with C, K (each group's K) a multiple of 128; waves 4, 6 or 8.
+void launch_fp8_gemm_1d1d(bool k_grouped, int waves, const Fp8GemmArgs& args, hipStream_t stream);
 
 // Arguments of the UE8M0 block-scaled kernel (A e4m3 or e2m1, B e4m3 or e2m1,
 // scales applied inside the scaled MFMA).

@@ -14,6 +14,8 @@ BF16/einsum/attention/Mega-MoE/cuBLASLt kernels are not provided.
 """
 from typing import Optional, Tuple
 
+import ctypes
+
 import torch
 
 from . import _ffi
@@ -213,6 +215,39 @@ def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d: torch.Tensor, masked_m: torch.Tens
     _check(_lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(
         _ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dm), int(expected_m), _ref(r),
         int(bool(disable_ue8m0_cast)), _ffi.stream_of(d)))
+
+
+def _k_grouped(entry, a, b, d, ks_cpu, grouped_layout, c, recipe, use_psum_layout, epilogue):
+    _check_epilogue(epilogue)
+    a_t, sfa = _pair(a, 'a')
+    b_t, sfb = _pair(b, 'b')
+    ks = [int(v) for v in (ks_cpu or [])]
+    ks_arr = (ctypes.c_int32 * max(1, len(ks)))(*ks) if ks else None
+    rec = (ctypes.c_int32 * 3)(*[int(v) for v in recipe]) if recipe is not None else None
+    da, dsa, db, dsb, dd, dl = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d), _desc(grouped_layout)
+    dc = _desc(c) if c is not None else None
+    _check(entry(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), ks_arr, len(ks), _ref(dl), _ref(dc), rec,
+                 int(bool(use_psum_layout)), _ffi.stream_of(d)))
+
+
+def k_grouped_fp8_gemm_nt_contiguous(a, b, d: torch.Tensor, ks_cpu, grouped_layout: torch.Tensor,
+                                     c: Optional[torch.Tensor] = None, recipe=(1, 1, 128),
+                                     compiled_dims: str = 'mn', use_psum_layout: bool = False,
+                                     epilogue=None) -> None:
+    """D[g] = C[g] + A_g @ B_g.T over K-slices of A and B, FP32 out with per-row
+    1x128 scales on both operands (reference csrc/apis/gemm.hpp:369-425)."""
+    _k_grouped(_lib.dg_k_grouped_fp8_gemm_nt_contiguous, a, b, d, ks_cpu, grouped_layout, c, recipe,
+               use_psum_layout, epilogue)
+
+
+def k_grouped_fp8_gemm_tn_contiguous(a, b, d: torch.Tensor, ks_cpu, grouped_layout: torch.Tensor,
+                                     c: Optional[torch.Tensor] = None, recipe=(1, 1, 128),
+                                     compiled_dims: str = 'mn', use_psum_layout: bool = False,
+                                     epilogue=None) -> None:
+    """MN-major form (reference csrc/apis/gemm.hpp:320-367, SM100 only there): raises
+    the reference's unsupported-architecture error, as its SM90 build does."""
+    _k_grouped(_lib.dg_k_grouped_fp8_gemm_tn_contiguous, a, b, d, ks_cpu, grouped_layout, c, recipe,
+               use_psum_layout, epilogue)
 
 
 # Aliases (reference csrc/apis/gemm.hpp:920-930)

@@ -102,7 +102,10 @@ int dg_shutdown(void);
  *   d    [M, N] bf16 or fp32, row-major
  *   c    NULL, or [M, N] with d's dtype (may alias d: in-place accumulate)
  * disable_ue8m0_cast: reference flag (csrc/apis/gemm.hpp:88); FP32 SFs of the
- * (1,128,128) recipe always take the FP32-scale path. */
+ * (1,128,128) recipe always take the FP32-scale path. FP32 SFs of the (1,1,128)
+ * recipe (sfb [N, ceil(K/128)], one scale per B row: the reference's SM90
+ * "1D1D" weight-gradient kernel, csrc/apis/gemm.hpp:119-122) need an FP32 d
+ * and a c (csrc/jit_kernels/impls/sm90_fp8_gemm_1d1d.hpp:91), and K % 128 == 0. */
 int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa,
                        const dg_tensor* b, const dg_tensor* sfb,
                        const dg_tensor* d, const dg_tensor* c,
@@ -144,6 +147,40 @@ int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa
                                         int32_t expected_m,
                                         const dg_recipe* recipe,
                                         int32_t disable_ue8m0_cast,
+                                        void* stream);
+
+/* K-grouped GEMM (weight gradients of MoE experts).
+ * Replaces k_grouped_fp8_gemm_nt_contiguous (csrc/apis/gemm.hpp:369-425,
+ * registered :903-910): for every group g, D[g] = C[g] + A_g @ B_g^T with
+ *   a    e4m3, contiguous, sum(K_g) * M elements: A_g [M, K_g] row-major, one after another
+ *   b    e4m3, contiguous, sum(K_g) * N elements: B_g [N, K_g] likewise
+ *   sfa  FP32 [M, sum(K_g)/128], sfb FP32 [N, sum(K_g)/128] (any strides): group g
+ *        owns the K-block columns [sum_{j<g} K_j / 128, +K_g / 128)
+ *   d, c FP32 [G, M, N] contiguous (c required, may alias d)
+ *   ks_cpu    host int32 [num_ks == G], each K_g a multiple of 128 (0 allowed)
+ *   grouped_layout  device int32 [G] holding the same K_g
+ *   recipe    NULL or int32[3] == {1, 1, 128}; use_psum_layout must be 0. */
+int dg_k_grouped_fp8_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor* sfa,
+                                        const dg_tensor* b, const dg_tensor* sfb,
+                                        const dg_tensor* d,
+                                        const int32_t* ks_cpu, int32_t num_ks,
+                                        const dg_tensor* grouped_layout,
+                                        const dg_tensor* c,
+                                        const int32_t* recipe,
+                                        int32_t use_psum_layout,
+                                        void* stream);
+
+/* Replaces k_grouped_fp8_gemm_tn_contiguous (csrc/apis/gemm.hpp:320-367,
+ * registered :895-902). The reference runs it on SM100 only; like its SM90
+ * build this returns DG_ERR_UNSUPPORTED. Same arguments as the NT form. */
+int dg_k_grouped_fp8_gemm_tn_contiguous(const dg_tensor* a, const dg_tensor* sfa,
+                                        const dg_tensor* b, const dg_tensor* sfb,
+                                        const dg_tensor* d,
+                                        const int32_t* ks_cpu, int32_t num_ks,
+                                        const dg_tensor* grouped_layout,
+                                        const dg_tensor* c,
+                                        const int32_t* recipe,
+                                        int32_t use_psum_layout,
                                         void* stream);
 
 /* ---------------------------------------------------------------- SF layouts */

@@ -20,6 +20,12 @@ Functions and what they follow:
 * ``gemm_masked``          -- rows r < masked_m[g] of group g are computed
                               (``scheduler/gemm.cuh:188-204,301-302``); the rest
                               stay untouched.
+* ``gemm_k_grouped``       -- ``csrc/apis/gemm.hpp:369-425`` with the data layout of
+                              ``tests/generators.py:488-548`` (K-major branch): group
+                              g multiplies the K-slice [sum_{j<g} K_j, +K_g) of A
+                              and B, each stored [M, K_g] / [N, K_g] row-major one
+                              after another; SF columns are the same K-slice in
+                              128-blocks; D[g] = C[g] + A_g.B_g^T.
 * ``mn_major_tma_aligned`` -- ``csrc/jit_kernels/impls/smxx_layout.hpp:60-106``:
                               values unchanged, strides (align(mn,4)*sf_k, 1, align(mn,4)).
 * ``pack_ue8m0_mn_major``  -- ``tests/test_layout.py:20-42``: exponent bytes, four
@@ -102,6 +108,33 @@ def gemm_masked(a_deq: np.ndarray, b_deq: np.ndarray, masked_m: np.ndarray):
         if r > 0:
             d[i, :r] = a_deq[i, :r].astype(np.float64) @ b_deq[i].astype(np.float64).T
     return d, valid
+
+
+def k_grouped_slices(flat: np.ndarray, ks, mn: int):
+    """Flat K-grouped operand [sum(ks) * mn] -> list of [mn, K_g] row-major views."""
+    out, off = [], 0
+    for k in ks:
+        out.append(flat[off * mn:(off + k) * mn].reshape(mn, k))
+        off += k
+    return out
+
+
+def gemm_k_grouped(a_codes_flat, sfa, b_codes_flat, sfb, ks, c, dequant):
+    """K-grouped D = C + A_g.B_g^T, float64. a_codes_flat [sum_k*M] codes, sfa [M,
+    sum_k/128]; ``dequant(codes [mn, K_g], sf [mn, K_g/128])`` -> float32."""
+    g, m, n = c.shape
+    a_g = k_grouped_slices(a_codes_flat, ks, m)
+    b_g = k_grouped_slices(b_codes_flat, ks, n)
+    out = np.array(c, dtype=np.float64, copy=True)
+    kb0 = 0
+    for i, k in enumerate(ks):
+        if k:
+            kb = k // 128
+            a_deq = dequant(a_g[i], sfa[:, kb0:kb0 + kb])
+            b_deq = dequant(b_g[i], sfb[:, kb0:kb0 + kb])
+            out[i] += a_deq.astype(np.float64) @ b_deq.astype(np.float64).T
+            kb0 += kb
+    return out
 
 
 def tma_aligned_size(x: int, element_size: int) -> int:

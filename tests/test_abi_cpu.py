@@ -152,12 +152,62 @@ def test_rejects_unaligned_operand():
     assert st == _ffi.DG_ERR_INVALID and '16-byte aligned' in msg
 
 
-def test_unsupported_1d1d_fp32_recipe():
+def test_1d1d_recipe_host_checks():
+    """(1, 1, 128) with FP32 SFs is the 1D1D path: FP32 D and C required
+    (sm90_fp8_gemm_1d1d.hpp:91), K % 128 == 0 here."""
     a, sfa, b, _, d = good_dense()
     sfb = fake((512, 8), _ffi.DG_F32)
     r = _ffi.recipe_struct(None, (1, 128), (1, 128))
-    st, msg = call_nt(a, sfa, b, sfb, d, recipe=r)
-    assert st == _ffi.DG_ERR_UNSUPPORTED and '1D1D' in msg
+    st, msg = call_nt(a, sfa, b, sfb, d, recipe=r)               # bf16 D, no C
+    assert st == _ffi.DG_ERR_INVALID and 'o.c != nullptr' in msg
+    d32 = fake((256, 512), _ffi.DG_F32)
+    st, msg = call_nt(a, sfa, b, sfb, d32, recipe=r)             # FP32 D, no C
+    assert st == _ffi.DG_ERR_INVALID and 'o.c != nullptr' in msg
+    m, n, k = 256, 512, 1000
+    st, msg = call_nt(fake((m, k), _ffi.DG_E4M3), fake((m, 8), _ffi.DG_F32), fake((n, k), _ffi.DG_E4M3),
+                      fake((n, 8), _ffi.DG_F32), d32, c=d32, recipe=r)
+    assert st == _ffi.DG_ERR_UNSUPPORTED and 'multiple of 128' in msg
+
+
+def call_kg(a, sfa, b, sfb, d, ks, layout, c, recipe=(1, 1, 128), psum=0, tn=False):
+    arr = (ctypes.c_int32 * max(1, len(ks)))(*ks)
+    rec = (ctypes.c_int32 * 3)(*recipe)
+    fn = _ffi.lib.dg_k_grouped_fp8_gemm_tn_contiguous if tn else _ffi.lib.dg_k_grouped_fp8_gemm_nt_contiguous
+    st = fn(ctypes.byref(a), ctypes.byref(sfa), ctypes.byref(b), ctypes.byref(sfb), ctypes.byref(d), arr, len(ks),
+            ctypes.byref(layout), ctypes.byref(c) if c else None, rec, psum, None)
+    return st, _ffi.lib.dg_last_error().decode()
+
+
+def test_k_grouped_host_checks():
+    """The reference's argument checks of k_grouped_fp8_gemm_nt_contiguous
+    (csrc/apis/gemm.hpp:369-404, check_k_grouped_args :55-76), all on the host."""
+    g, m, n, ks = 2, 128, 256, [256, 128]
+    sk = sum(ks)
+
+    def ops(ks_=ks):
+        s = sum(ks_)
+        return (fake((s * m,), _ffi.DG_E4M3), fake((m, s // 128), _ffi.DG_F32), fake((s * n,), _ffi.DG_E4M3),
+                fake((n, s // 128), _ffi.DG_F32), fake((g, m, n), _ffi.DG_F32))
+    layout = fake((g,), _ffi.DG_I32)
+    a, sfa, b, sfb, d = ops()
+    st, msg = call_kg(a, sfa, b, sfb, d, ks, layout, d, recipe=(1, 1, 32))
+    assert st == _ffi.DG_ERR_INVALID and 'r2 == 128' in msg
+    st, msg = call_kg(a, sfa, b, sfb, d, ks, layout, d, psum=1)
+    assert st == _ffi.DG_ERR_INVALID and 'use_psum_layout' in msg
+    st, msg = call_kg(a, sfa, b, sfb, d, ks, layout, None)
+    assert st == _ffi.DG_ERR_INVALID and 'c != nullptr' in msg
+    st, msg = call_kg(a, sfa, b, sfb, d, [256, 100], layout, d)
+    assert st == _ffi.DG_ERR_INVALID and '% 128' in msg
+    st, msg = call_kg(a, sfa, b, sfb, d, [256], layout, d)
+    assert st == _ffi.DG_ERR_INVALID and 'num_ks' in msg
+    st, msg = call_kg(fake((sk * m + 16,), _ffi.DG_E4M3), sfa, b, sfb, d, ks, layout, d)
+    assert st == _ffi.DG_ERR_INVALID and 'sum_k * m' in msg
+    st, msg = call_kg(a, sfa, b, sfb, fake((g, m, n), _ffi.DG_BF16), ks, layout, d)
+    assert st == _ffi.DG_ERR_INVALID and 'DG_F32' in msg
+    st, msg = call_kg(a, fake((m, 2), _ffi.DG_F32), b, sfb, d, ks, layout, d)
+    assert st == _ffi.DG_ERR_INVALID and 'sum_k / 128' in msg
+    st, msg = call_kg(a, sfa, b, sfb, d, ks, layout, d, tn=True)
+    assert st == _ffi.DG_ERR_UNSUPPORTED and 'Unsupported' in msg
 
 
 def test_ue8m0_path_rejects_disable_cast():

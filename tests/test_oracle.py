@@ -186,6 +186,50 @@ def test_gemm_nt_triple_loop():
             assert abs(d[i, j] - s) < 1e-12
 
 
+def test_k_grouped_brute_force_tiny():
+    """gemm_k_grouped against scalar loops over the flat layout: group g's A_g is the
+    [M, K_g] row-major block at element offset sum_{j<g} K_j * M, its scales the
+    K-block columns of the same slice; an empty group leaves C as it is."""
+    rng = np.random.default_rng(11)
+    ks, m, n = [128, 0, 256], 3, 2
+    sum_k = sum(ks)
+    a = rng.integers(0, 256, size=sum_k * m).astype(np.uint8)
+    b = rng.integers(0, 256, size=sum_k * n).astype(np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0                       # no NaN codes
+    b[(b & 0x7F) == 0x7F] = 0
+    sfa = rng.uniform(0.5, 2.0, size=(m, sum_k // 128)).astype(np.float32)
+    sfb = rng.uniform(0.5, 2.0, size=(n, sum_k // 128)).astype(np.float32)
+    c = rng.standard_normal((len(ks), m, n))
+    d = ogemm.gemm_k_grouped(a, sfa, b, sfb, ks, c, oquant.dequant_per_token)
+    val = fp8.E4M3_TABLE
+    off = 0
+    for g, k in enumerate(ks):
+        for i in range(m):
+            for j in range(n):
+                s = c[g, i, j]
+                for kk in range(k):
+                    kb = (off + kk) // 128
+                    av = np.float32(val[a[off * m + i * k + kk]]) * sfa[i, kb]
+                    bv = np.float32(val[b[off * n + j * k + kk]]) * sfb[j, kb]
+                    s += float(av) * float(bv)
+                assert abs(d[g, i, j] - s) <= 1e-9 * max(1.0, abs(s))
+        off += k
+    assert np.array_equal(d[1], c[1])
+
+
+def test_k_grouped_single_group_is_dense():
+    rng = np.random.default_rng(12)
+    m, n, k = 5, 4, 384
+    qa = rng.integers(0, 0x7E, size=(m, k)).astype(np.uint8)
+    qb = rng.integers(0, 0x7E, size=(n, k)).astype(np.uint8)
+    sfa = rng.uniform(0.1, 1.0, size=(m, 3)).astype(np.float32)
+    sfb = rng.uniform(0.1, 1.0, size=(n, 3)).astype(np.float32)
+    c = rng.standard_normal((1, m, n))
+    d = ogemm.gemm_k_grouped(qa.reshape(-1), sfa, qb.reshape(-1), sfb, [k], c, oquant.dequant_per_token)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(qa, sfa), oquant.dequant_per_token(qb, sfb), c[0])
+    assert np.array_equal(d[0], ref)
+
+
 def test_gemm_closed_form_ones():
     """A all 1.0 with SF 2, B all 0.5 with SF 0.25, K = 256: every D = 256 * 2 * 0.125 = 64."""
     m, n, k = 5, 130, 256
