@@ -335,18 +335,19 @@ bool is_1d1d(const Operands& o, const Recipe& r) {
            r.gran_k_b == 128;
 }
 
-// Waves (block_n / 32) of the 1D1D kernel: whole rounds of one workgroup per
-// CU, weighted by the measured per-CU throughput of each width.
-int fp8_1d1d_waves(int64_t m, int64_t n, int64_t groups, int cus) {
-    static const struct { int nw; double eff; } cands[] = {{8, 1.0}, {6, 0.9}, {4, 0.7}};
-    int best_nw = 8;
-    double best = 1e300;
-    for (const auto& c : cands) {
-        const int64_t tiles = ceil_div(m, (int64_t)128) * ceil_div(n, (int64_t)(32 * c.nw)) * groups;
-        const double cost = (double)ceil_div(tiles, (int64_t)cus) * 32 * c.nw / c.eff;
-        if (cost < best - 1e-9) best = cost, best_nw = c.nw;
+// The 1D1D kernels: the 256 x 128 LDS-pipelined one (variant 7, the default) or
+// the 128-row streaming one (variant 6, by tile override).
+void launch_1d1d(bool k_grouped, const Fp8GemmArgs& args, hipStream_t stream, int64_t m, int64_t n, int64_t k,
+                 int64_t groups) {
+    const GemmKind kind = k_grouped ? kKGrouped : kNormal;
+    if (g_tile_variant.load() == 6) {
+        const int waves = g_tile_n.load() / 32;
+        record_config("fp8_gemm_1d1d", kind, TileConfig{128, 32 * waves, 6}, m, n, k, groups);
+        launch_fp8_gemm_1d1d(k_grouped, waves, args, stream);
+        return;
     }
-    return best_nw;
+    record_config("fp8_gemm_1d1d", kind, TileConfig{256, 128, 7}, m, n, k, groups);
+    launch_fp8_gemm_1d1d_pipe(k_grouped, args, stream);
 }
 
 bool is_ue8m0_path(const Operands& o, const Recipe& r) {
@@ -504,11 +505,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.lda = o.a.stride(-2), args.ldb = o.b.stride(-2), args.ldd = o.d.stride(-2), args.ldc = cv.stride(-2);
         args.sfa_sm = o.sfa.stride(-2), args.sfa_sk = o.sfa.stride(-1);
         args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
-        int cus = 256;
-        try { cus = num_sms_now(); } catch (const Error&) {}
-        const int waves = fp8_1d1d_waves(m, n, 1, cus);
-        record_config("fp8_gemm_1d1d", kind, TileConfig{128, 32 * waves, 6}, m, n, k, 1);
-        launch_fp8_gemm_1d1d(false, waves, args, stream);
+        launch_1d1d(false, args, stream, m, n, k, 1);
         return;
     }
     DG_UNSUPPORTED("Unsupported architecture or scaling factor types");
@@ -797,11 +794,7 @@ void k_grouped_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor*
     args.ldd = n, args.ldc = n, args.d_gs = m * n, args.c_gs = m * n;
     args.sfa_sm = sfa.stride(0), args.sfa_sk = sfa.stride(1);
     args.sfb_sn = sfb.stride(0), args.sfb_sk = sfb.stride(1);
-    int cus = 256;
-    try { cus = num_sms_now(); } catch (const Error&) {}
-    const int waves = fp8_1d1d_waves(m, n, g, cus);
-    record_config("fp8_gemm_1d1d", kKGrouped, TileConfig{128, 32 * waves, 6}, m, n, sum_k, g);
-    launch_fp8_gemm_1d1d(true, waves, args, stream);
+    launch_1d1d(true, args, stream, m, n, sum_k, g);
 }
 
 }  // namespace
@@ -946,6 +939,8 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
                         : variant == 2 ? fp8_1d2d_v2_tile_supported(block_m, block_n)
                         : variant == 5 ? (block_m == kMaskedStreamRows && block_n % 32 == 0 && block_n >= 128 &&
                                           block_n <= 256)
+                        : variant == 6 ? (block_m == 128 && (block_n == 128 || block_n == 192 || block_n == 256))
+                        : variant == 7 ? (block_m == 256 && block_n == 128)
                                        : (variant == 4 && block_m == 256 && block_n == 256);
         if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;

@@ -58,7 +58,10 @@ __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2))
 // (scheduler/gemm.cuh:185-272, masked group walk :188-204, psum walk :205-225;
 // decode_tile_persistent). Otherwise one workgroup per tile and the hardware
 // dispatcher starts the next tile as a CU frees up.
-template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT, int PERSIST>
+// SB1D: per-row B scales (the 1D1D recipe, SFB [N, K/128]): each stage also
+// carries the SFB of its BN columns, and every output column gets its own scale.
+template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT, int PERSIST,
+          int SB1D = 0>
 __global__ void __launch_bounds__(WGM * WGN * 64, 1)
 fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const int num_n_blocks,
                           const int raster_gm) {
@@ -70,19 +73,22 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     constexpr int A_INSTR = BM / (8 * NW);     // 1 KB (8-row) wave loads per stage for A
     constexpr int B_INSTR = BN / (8 * NW);
     static_assert(A_INSTR * 8 * NW == BM && B_INSTR * 8 * NW == BN, "tile rows per wave load");
-    constexpr int LOADS_PER_STAGE = A_INSTR + B_INSTR + 1;   // + one SFA load
+    constexpr int LOADS_PER_STAGE = A_INSTR + B_INSTR + 1 + SB1D;   // + one SFA (and SFB) load
     constexpr int SA_OFF = (BM + BN) * kBK;
     constexpr int SA_ROWS_PER_WAVE = BM / NW;  // SFA rows loaded by each wave (<= 64)
-    constexpr int STAGE_BYTES = SA_OFF + NW * 256;
+    constexpr int SB_OFF = SA_OFF + NW * 256;   // SB1D: SFB of the stage's BN columns
+    constexpr int SB_SEGS = (BN + 63) / 64;
+    constexpr int STAGE_BYTES = SB_OFF + (SB1D ? BN * 4 : 0);
+    static_assert(!SB1D || (!KT && KIND != kMasked && KIND != kContiguous && KIND != kPsum), "1D1D: dense / K-grouped");
     // When every wave's N range sits in one 128-row SFB block, sa and sb fold into
     // one factor per row; otherwise (e.g. 192-wide tiles) each 32-column sub-tile
     // looks up its own block.
-    constexpr bool SPLIT_SB = !(BN % 128 == 0 && WN <= 128 && 128 % WN == 0);
+    constexpr bool SPLIT_SB = !SB1D && !(BN % 128 == 0 && WN <= 128 && 128 % WN == 0);
     static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
     static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
-    __shared__ float s_sfb[2][kMaxKBlocks];   // SFB of the block's (at most two) 128-row N groups
+    __shared__ float s_sfb[SB1D ? 1 : 2][SB1D ? 1 : kMaxKBlocks];   // SFB of the block's (at most two) 128-row N groups
     __shared__ int s_flag;
     __shared__ int s_half_valid[2];
 
@@ -141,14 +147,25 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
         }
     }
 
-    const uint8_t* __restrict__ a_base =
-        p.a + ((KIND == kMasked) ? (int64_t)t.g * p.a_gs : 0) + (int64_t)m0 * p.lda;
-    const float* __restrict__ sa_base =
-        p.sfa + ((KIND == kMasked) ? (int64_t)t.g * p.sfa_gs : 0) + (int64_t)m0 * p.sfa_sm;
+    // K-grouped: group g multiplies the K-slice [k_off, k_off + K_g) of A and B,
+    // stored [M, K_g] / [N, K_g] row-major one group after another; its scales
+    // are the same slice of K-block columns.
+    int64_t lda = p.lda, ldb = p.ldb, k_off = 0;
+    int kdim = p.k;
+    if constexpr (KIND == kKGrouped) {
+        const __attribute__((address_space(4))) int32_t* ks = (const __attribute__((address_space(4))) int32_t*)p.layout;
+        for (int j = 0; j < t.g; ++j) k_off += ks[j];
+        kdim = ks[t.g];
+        lda = ldb = kdim;
+    }
+    const uint8_t* __restrict__ a_base = p.a + ((KIND == kMasked) ? (int64_t)t.g * p.a_gs : 0) + k_off * p.m +
+                                         (int64_t)m0 * lda;
+    const float* __restrict__ sa_base = p.sfa + ((KIND == kMasked) ? (int64_t)t.g * p.sfa_gs : 0) +
+                                        (k_off / kBK) * p.sfa_sk + (int64_t)m0 * p.sfa_sm;
 
     const int a_rows = min(BM, t.row_end - m0);
     const int b_rows = min(BN, p.n - n0);
-    const int num_kb = (p.k + kBK - 1) / kBK;
+    const int num_kb = (kdim + kBK - 1) / kBK;
     const int my_group = ((n0 & 127) + wn * WN) >> 7;
 
     // One pass of the tile: the whole K loop and the epilogue. Written as a lambda
@@ -167,9 +184,11 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
         wave_computes = __builtin_amdgcn_readfirstlane((int)(wm * WM < a_rows && p.m >= 0)) != 0;
     else
         wave_computes = (npass == 1 || (wm * WM) >> 7 == pass) && p.m >= 0;
-    const uint8_t* __restrict__ b_base = p.b + (int64_t)expert * p.b_gs + (int64_t)n0 * p.ldb;
+    const uint8_t* __restrict__ b_base = p.b + (int64_t)expert * p.b_gs + k_off * p.n + (int64_t)n0 * ldb;
+    const float* __restrict__ sb_base = p.sfb + (int64_t)expert * p.sfb_gs + (k_off / kBK) * p.sfb_sk +
+                                        (int64_t)n0 * p.sfb_sn;
     if (pass > 0) __syncthreads();   // every wave is done with the stage ring and s_sfb of the previous pass
-    {
+    if constexpr (!SB1D) {
         const float* sfb_g = p.sfb + (int64_t)expert * p.sfb_gs;
         const int last_row = (p.n - 1) >> 7;
         for (int idx = tid; idx < 2 * num_kb; idx += NT) {
@@ -225,6 +244,8 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const uint32_t chunk_off = (pc ^ swz_g((wave & 1) * 8 + rs)) << 4;
     const int sa_row = wave * SA_ROWS_PER_WAVE + lane;
     const uint32_t voff_sa = (uint32_t)(min(sa_row, a_rows - 1) * p.sfa_sm) * 4u;
+    const int sb_seg = min(wave, SB_SEGS - 1);   // SB1D: surplus waves repeat the last segment
+    const uint32_t voff_sb = SB1D ? (uint32_t)(min(sb_seg * 64 + lane, b_rows - 1) * p.sfb_sn) * 4u : 0u;
     auto clamped_voff = [&](int seg, int rows, int ld) {
         const int r = min(seg * 8 + launder(rs), rows - 1);
         return (uint32_t)r * (uint32_t)ld + chunk_off;
@@ -239,22 +260,25 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
 #pragma unroll
             for (int i = 0; i < A_INSTR; ++i) {
                 const int seg = i * NW + wave;
-                dma16_saddr(a_kb, clamped_voff(seg, a_rows, p.lda), stage_lds + seg * 1024);
+                dma16_saddr(a_kb, clamped_voff(seg, a_rows, lda), stage_lds + seg * 1024);
             }
 #pragma unroll
             for (int i = 0; i < B_INSTR; ++i) {
                 const int seg = i * NW + wave;
-                dma16_saddr(b_kb, clamped_voff(seg, b_rows, p.ldb), stage_lds + BM * kBK + seg * 1024);
+                dma16_saddr(b_kb, clamped_voff(seg, b_rows, ldb), stage_lds + BM * kBK + seg * 1024);
             }
             dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
                        stage_lds + SA_OFF + wave * 256);
+            if constexpr (SB1D)
+                dma4_saddr(reinterpret_cast<const uint8_t*>(sb_base + (int64_t)kb * p.sfb_sk), voff_sb,
+                           stage_lds + SB_OFF + sb_seg * 256);
         } else {
 #pragma unroll
             for (int i = 0; i < A_INSTR; ++i) {
                 const int seg = i * NW + wave;
                 const int r = seg * 8 + launder(rs);
                 const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
-                const void* src = (r < a_rows && k < p.k) ? (const void*)(a_base + (int64_t)r * p.lda + k)
+                const void* src = (r < a_rows && k < kdim) ? (const void*)(a_base + (int64_t)r * lda + k)
                                                           : (const void*)g_zero_page;
                 dma16_vaddr(src, stage_lds + seg * 1024);
             }
@@ -263,7 +287,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                 const int seg = i * NW + wave;
                 const int r = seg * 8 + launder(rs);
                 const int k = kb * kBK + ((pc ^ swz_g(r)) << 4);
-                const void* src = (r < b_rows && k < p.k) ? (const void*)(b_base + (int64_t)r * p.ldb + k)
+                const void* src = (r < b_rows && k < kdim) ? (const void*)(b_base + (int64_t)r * ldb + k)
                                                           : (const void*)g_zero_page;
                 dma16_vaddr(src, stage_lds + BM * kBK + seg * 1024);
             }
@@ -280,6 +304,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     i32x8 opB[SN][2], opA[2][2];
     float sa_cur[SM];
     float scl[SPLIT_SB ? SM : 1][SPLIT_SB ? SN : 1];
+    float sbv[SB1D ? SN : 1][SB1D ? 16 : 1];   // SB1D: sb of the lane's 16 columns of each sub-tile
     // sa * sb of the lane's rows for K block kb (read at the top of the block's
     // compute; the stage slot is refilled only after the next barrier).
     auto load_scales = [&](int kb) {
@@ -289,7 +314,9 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
             const int r = wm * WM + i * 32 + lrow;
             const float sa = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
                                                              (r % SA_ROWS_PER_WAVE) * 4);
-            if constexpr (SPLIT_SB) {
+            if constexpr (SB1D) {
+                sa_cur[i] = sa;
+            } else if constexpr (SPLIT_SB) {
 #pragma unroll
                 for (int j = 0; j < SN; ++j)
                     scl[i][j] = sa * s_sfb[((n0 & 127) + wn * WN + j * 32) >> 7][kb];
@@ -297,10 +324,27 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                 sa_cur[i] = sa * s_sfb[my_group][kb];
             }
         }
+        if constexpr (SB1D) {
+            // columns 32j + 8q + 4lhalf + e of the wave's tile (the accumulator layout)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(sbase + SB_OFF +
+                                                                    (wn * WN + j * 32 + q * 8 + lhalf * 4) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sbv[j][q * 4 + e] = v[e];
+                }
+        }
     };
     auto scale_of = [&](int i, int j) {
         if constexpr (SPLIT_SB) return scl[i][j];
         else return sa_cur[i];
+    };
+    // scale of element e of sub-tile (i, j)
+    auto sc = [&](int i, int j, int e) {
+        if constexpr (SB1D) return sa_cur[i] * sbv[j][e];
+        else return scale_of(i, j);
     };
     auto load_stage_frags = [&](int kb) {
         const uint8_t* sbase = smem + (kb % STAGES) * STAGE_BYTES;
@@ -397,13 +441,13 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                 const int pi = j > 0 ? i : i - 1;
                 if (pi >= 0) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) fin[pi][pj][e] = __builtin_fmaf(scale_of(pi, pj), acc[pj][e], fin[pi][pj][e]);
+                    for (int e = 0; e < 16; ++e) fin[pi][pj][e] = __builtin_fmaf(sc(pi, pj, e), acc[pj][e], fin[pi][pj][e]);
                 }
             }
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-            fin[SM - 1][SN - 1][e] = __builtin_fmaf(scale_of(SM - 1, SN - 1), acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
+            fin[SM - 1][SN - 1][e] = __builtin_fmaf(sc(SM - 1, SN - 1, e), acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
         }
     }
 
@@ -451,14 +495,14 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                         if (pi >= 0) {
 #pragma unroll
                             for (int e = 0; e < 16; ++e)
-                                fin[pi][pj][e] = __builtin_fmaf(scale_of(pi, pj), acc[pj][e], fin[pi][pj][e]);
+                                fin[pi][pj][e] = __builtin_fmaf(sc(pi, pj, e), acc[pj][e], fin[pi][pj][e]);
                         }
                     }
                 }
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
                     fin[SM - 1][SN - 1][e] =
-                        __builtin_fmaf(scale_of(SM - 1, SN - 1), acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
+                        __builtin_fmaf(sc(SM - 1, SN - 1, e), acc[SN - 1][e], fin[SM - 1][SN - 1][e]);
             }
         }
     }
@@ -472,11 +516,13 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     {
         using Epi = RowEpilogue<KIND, OUT_F32, HAS_C, SM, SN>;
         constexpr int REGION = (STAGES * STAGE_BYTES / NW) / 16 * 16;
-        const int64_t d_goff = (KIND == kMasked) ? (int64_t)t.g * p.d_gs : 0;
+        const int64_t d_goff = (KIND == kMasked || KIND == kKGrouped) ? (int64_t)t.g * p.d_gs : 0;
+        const void* c_g = (KIND == kKGrouped && HAS_C) ? (const void*)(static_cast<const float*>(p.c) + (int64_t)t.g * p.c_gs)
+                                                       : p.c;
         const int m_lo = npass == 2 ? m0 + pass * 128 : m0;
         const int m_hi = npass == 2 ? m_lo + 128 : m0 + BM;
         Epi::template run<Epi::rows_per_pass(REGION)>(fin, smem + wave * REGION, lane, t, p.m, p.layout,
-                                                      m0 + wm * WM, n0 + wn * WN, p.n, m_lo, m_hi, p.d, p.c, p.ldd,
+                                                      m0 + wm * WM, n0 + wn * WN, p.n, m_lo, m_hi, p.d, c_g, p.ldd,
                                                       p.ldc, d_goff);
     }
     };   // run_pass
@@ -548,7 +594,35 @@ void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
     }
 }
 
+// 1D1D recipe (SB1D), dense or K-grouped: FP32 D accumulating into C, K (or
+// each group's K) a multiple of 128.
+template <int KIND>
+void launch_1d1d_kind(const Fp8GemmArgs& a, hipStream_t stream) {
+    // 256 x 128 with four waves of 128 x 64: the per-column scales (16 more live
+    // registers per sub-tile column) do not fit the 256 registers of the
+    // eight-wave 256 x 256 tile.
+    constexpr int BM = 256, BN = 128;
+    const int num_n_blocks = (a.n + BN - 1) / BN;
+    const int num_m_blocks = (a.m + BM - 1) / BM;
+    int64_t grid = (int64_t)num_m_blocks * num_n_blocks;
+    if (KIND == kKGrouped) grid *= a.num_groups;
+    if (grid == 0) return;
+    DG_CHECK(grid < (int64_t)1 << 31);
+    DG_CHECK(a.out_f32 && a.c != nullptr && a.k % kBK == 0);
+    const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
+    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, 2, 2, 3, KIND, 1, 1, 0, 0, 1>), dim3((unsigned)grid),
+                       dim3(256), 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+    DG_HIP_CHECK(hipGetLastError());
+}
+
 }  // namespace
+
+void launch_fp8_gemm_1d1d_pipe(bool k_grouped, const Fp8GemmArgs& args, hipStream_t stream) {
+    if (k_grouped)
+        launch_1d1d_kind<kKGrouped>(args, stream);
+    else
+        launch_1d1d_kind<kNormal>(args, stream);
+}
 
 bool fp8_1d2d_v2_tile_supported(int bm, int bn) {
     return (bm == 256 && bn == 256) || (bm == 256 && bn == 192) || (bm == 256 && bn == 128) ||

@@ -112,6 +112,8 @@ void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& args, int waves, hipStream
 // The 1D1D (per-row B scales) kernel, dense or K-grouped (dg_gemm_fp8_1d1d.hip):
 // FP32 D with C, K (each group's K) a multiple of 128; waves 4, 6 or 8.
 void launch_fp8_gemm_1d1d(bool k_grouped, int waves, const Fp8GemmArgs& args, hipStream_t stream);
+// The same recipe on the 256 x 256 LDS-pipelined kernel (dg_gemm_fp8_pipe.hip).
+void launch_fp8_gemm_1d1d_pipe(bool k_grouped, const Fp8GemmArgs& args, hipStream_t stream);
 
 // Arguments of the UE8M0 block-scaled kernel (A e4m3 or e2m1, B e4m3 or e2m1,
 // scales applied inside the scaled MFMA).

@@ -95,7 +95,7 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
                                             uint16_t* zero_d, int64_t ldd, int* s_flag, int raster_gm = 0) {
     Tile t{};
     int tile = xcd_remap(blockIdx.x, gridDim.x);
-    if constexpr (KIND == kMasked) {
+    if constexpr (KIND == kMasked || KIND == kKGrouped) {
         const int per_group = num_m_blocks * num_n_blocks;
         t.g = tile / per_group;
         tile -= t.g * per_group;
@@ -110,6 +110,8 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
         t.row_end = min(m, layout[t.g]);
         t.expert = t.g;
         t.active = t.m0 < t.row_end;
+    } else if constexpr (KIND == kKGrouped) {
+        t.expert = 0;   // the group selects K-slices, not a B of its own (b_gs == 0)
     } else if constexpr (KIND == kContiguous) {
         // Expert of the block = max(0, m_indices[first row]) (scheduler/gemm.cuh:150-153);
         // a block whose rows are all padding does nothing.
@@ -249,7 +251,7 @@ template <int KIND>
 __device__ __forceinline__ void row_predicate(const Tile& t, int m, const int32_t* __restrict__ layout, int mrow,
                                               bool& store, bool& zero) {
     zero = false;
-    if constexpr (KIND == kNormal) {
+    if constexpr (KIND == kNormal || KIND == kKGrouped) {
         store = mrow < m;
     } else if constexpr (KIND == kMasked) {
         store = mrow < t.row_end;

@@ -166,3 +166,32 @@ def test_k_grouped_empty_and_checks():
         deep_gemm.k_grouped_fp8_gemm_nt_contiguous(a, b, d, [100, 284], layout, d)
     with pytest.raises(RuntimeError, match='Unsupported'):
         deep_gemm.k_grouped_fp8_gemm_tn_contiguous(a, b, d, ks, layout, d)
+
+
+@pytest.mark.parametrize('kg', [False, True])
+def test_1d1d_kernels_bitwise_equal(kg):
+    """The 256 x 128 pipelined 1D1D kernel (variant 7, the default) and the 128-row
+    streaming one (variant 6) compute the same bits."""
+    outs = []
+    for v, tile in [(7, (256, 128)), (6, (128, 256)), (6, (128, 192))]:
+        deep_gemm.set_tile_override(tile[0], tile[1], variant=v)
+        try:
+            if kg:
+                ks, m, n = [384, 0, 256, 128], 300, 456
+                qa, sfa, qb, sfb, c_np = k_grouped_inputs(ks, m, n, 9)
+                d = f32(c_np)
+                layout = torch.tensor(ks, dtype=torch.int32, device=DEV)
+                deep_gemm.k_grouped_fp8_gemm_nt_contiguous((e4m3(qa), f32(sfa)), (e4m3(qb), f32(sfb)), d, ks,
+                                                           layout, d)
+            else:
+                qa, sfa, qb, sfb = dense_1d1d(520, 600, 1152, 8)
+                d = f32(np.random.default_rng(3).standard_normal((520, 600)))
+                deep_gemm.fp8_gemm_nt((e4m3(qa), f32(sfa)), (e4m3(qb), f32(sfb)), d, c=d, recipe=(1, 1, 128))
+            cfg = deep_gemm.get_last_config()
+        finally:
+            deep_gemm.set_tile_override(0, 0)
+        torch.cuda.synchronize()
+        assert f' v{v} ' in cfg, cfg
+        outs.append(d)
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32))
