@@ -49,6 +49,7 @@ using namespace dev;
 
 constexpr int kBK = 128;
 constexpr int kMaxKBlocks = 1024;   // K up to 131072 on this path (the host routes longer K elsewhere)
+constexpr int kMaxKBlocksKsa = 256;
 
 __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
@@ -60,8 +61,14 @@ __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2))
 // dispatcher starts the next tile as a CU frees up.
 // SB1D: per-row B scales (the 1D1D recipe, SFB [N, K/128]): each stage also
 // carries the SFB of its BN columns, and every output column gets its own scale.
+// KSA (0, 4 or 8): SFA is K-major (the layout per_token_cast_to_fp8 writes: a row's
+// scales for consecutive K blocks are adjacent) and K is a multiple of 128 * KSA.
+// A per-stage 4-byte load per row would then touch one cache line per row per K
+// block, as many L2 requests as the whole A and B tiles; instead each row's scales
+// for KSA K blocks (a "scale group", 16 or 32 bytes, one L2 request) are fetched
+// into a three-slot LDS ring, and the stages carry no SFA.
 template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT, int PERSIST,
-          int SB1D = 0>
+          int SB1D = 0, int KSA = 0>
 __global__ void __launch_bounds__(WGM * WGN * 64, 1)
 fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const int num_n_blocks,
                           const int raster_gm) {
@@ -73,13 +80,21 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     constexpr int A_INSTR = BM / (8 * NW);     // 1 KB (8-row) wave loads per stage for A
     constexpr int B_INSTR = BN / (8 * NW);
     static_assert(A_INSTR * 8 * NW == BM && B_INSTR * 8 * NW == BN, "tile rows per wave load");
-    constexpr int LOADS_PER_STAGE = A_INSTR + B_INSTR + 1 + SB1D;   // + one SFA (and SFB) load
+    constexpr int LOADS_PER_STAGE = A_INSTR + B_INSTR + (KSA ? 0 : 1) + SB1D;   // + one SFA (and SFB) load
     constexpr int SA_OFF = (BM + BN) * kBK;
     constexpr int SA_ROWS_PER_WAVE = BM / NW;  // SFA rows loaded by each wave (<= 64)
     constexpr int SB_OFF = SA_OFF + NW * 256;   // SB1D: SFB of the stage's BN columns
     constexpr int SB_SEGS = (BN + 63) / 64;
     constexpr int STAGE_BYTES = SB_OFF + (SB1D ? BN * 4 : 0);
     static_assert(!SB1D || (!KT && KIND != kMasked && KIND != kContiguous && KIND != kPsum), "1D1D: dense / K-grouped");
+    // (with two stages every hand-off waits for all of a wave's loads, so the group
+    // loads, issued by some waves only, need no place in the vmcnt accounting)
+    static_assert(KSA == 0 || KSA == 4 || KSA == 8, "scale group size");
+    constexpr int KSA_LPR = KSA ? KSA / 4 : 1;         // lanes per row (16 bytes each)
+    constexpr int KSA_RPS = 64 / KSA_LPR;              // rows per 1 KB segment of a group
+    // one segment per K block of the group, a 64-lane segment split over the waves
+    static_assert(!KSA || (STAGES == 2 && !KT && !SB1D && !PERSIST && BM / KSA_RPS == KSA && NW == 8),
+                  "K-major SFA groups");
     // When every wave's N range sits in one 128-row SFB block, sa and sb fold into
     // one factor per row; otherwise (e.g. 192-wide tiles) each 32-column sub-tile
     // looks up its own block.
@@ -88,7 +103,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
-    __shared__ float s_sfb[SB1D ? 1 : 2][SB1D ? 1 : kMaxKBlocks];   // SFB of the block's (at most two) 128-row N groups
+    // SFB of the block's (at most two) 128-row N groups (KSA kernels: K up to 32768,
+    // which leaves room for the scale-group ring)
+    __shared__ float s_sfb[SB1D ? 1 : 2][SB1D ? 1 : KSA ? kMaxKBlocksKsa : kMaxKBlocks];
+    __shared__ __attribute__((aligned(16))) float s_sag[KSA ? 3 : 1][KSA ? BM : 1][KSA ? KSA : 1];   // [slot][row][kb % KSA]
     __shared__ int s_flag;
     __shared__ int s_half_valid[2];
 
@@ -252,6 +270,31 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     };
 
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    // KSA: scale group g (K blocks KSA*g .. KSA*g + KSA - 1) sits in slot g % 3, row
+    // r at byte r * 4 * KSA, and is made of KSA segments of KSA_RPS rows (1 KB).
+    // Group 0 is loaded whole before the loop. Segment j of group g + 1 is loaded at
+    // the top of block KSA*g + j - 1 (segment 0 of group 1 before the loop), every
+    // wave its 8 lanes of it, so each wave issues exactly one load per block there:
+    // the hand-off waits then leave that load in flight (vmcnt(1)) and retire it at
+    // the next hand-off, before the group's first block at the latest. Its slot last
+    // held group g - 2, long done. Past the last group the loads repeat the last
+    // group's segments into its own slot (the same bytes).
+    const uint32_t sag_lds = __builtin_amdgcn_readfirstlane(lds_address(reinterpret_cast<const uint8_t*>(&s_sag[0][0][0])));
+    const int ksa_last = KSA ? num_kb / (KSA ? KSA : 1) - 1 : 0;
+    const uint64_t seg_exec = KSA ? (0xFFull << (8 * wave)) : 0ull;
+    // segment j of group g (only this wave's 8 lanes when `whole` is false)
+    auto issue_segment = [&](int g, int j, bool whole) {
+        const int row = j * KSA_RPS + launder(lane) / KSA_LPR;
+        const uint32_t voff = (uint32_t)(min(row, a_rows - 1) * p.sfa_sm) * 4u + (lane % KSA_LPR) * 16u;
+        dma16_saddr_masked(whole ? __builtin_amdgcn_read_exec() : seg_exec,
+                           reinterpret_cast<const uint8_t*>(sa_base + KSA * g), voff,
+                           sag_lds + (g % 3) * (BM * KSA * 4) + j * 1024);
+    };
+    // the load at the top of block kb (kb = -1: before the loop)
+    auto issue_block_segment = [&](int kb) {
+        const int ks = kb + 1;
+        issue_segment(min(ks / (KSA ? KSA : 1) + 1, ksa_last), ks % (KSA ? KSA : 1), false);
+    };
     auto issue_stage = [&](int kb, int st) {
         const uint32_t stage_lds = smem_lds + st * STAGE_BYTES;
         if constexpr (!KT) {
@@ -267,8 +310,9 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                 const int seg = i * NW + wave;
                 dma16_saddr(b_kb, clamped_voff(seg, b_rows, ldb), stage_lds + BM * kBK + seg * 1024);
             }
-            dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
-                       stage_lds + SA_OFF + wave * 256);
+            if constexpr (!KSA)
+                dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
+                           stage_lds + SA_OFF + wave * 256);
             if constexpr (SB1D)
                 dma4_saddr(reinterpret_cast<const uint8_t*>(sb_base + (int64_t)kb * p.sfb_sk), voff_sb,
                            stage_lds + SB_OFF + sb_seg * 256);
@@ -312,8 +356,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
 #pragma unroll
         for (int i = 0; i < SM; ++i) {
             const int r = wm * WM + i * 32 + lrow;
-            const float sa = *reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
-                                                             (r % SA_ROWS_PER_WAVE) * 4);
+            const float* sa_p = reinterpret_cast<const float*>(sbase + SA_OFF + (r / SA_ROWS_PER_WAVE) * 256 +
+                                                               (r % SA_ROWS_PER_WAVE) * 4);
+            if constexpr (KSA) sa_p = &s_sag[(kb / KSA) % 3][r][kb % KSA];
+            const float sa = *sa_p;
             if constexpr (SB1D) {
                 sa_cur[i] = sa;
             } else if constexpr (SPLIT_SB) {
@@ -364,7 +410,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     auto wait_stage = [&](int s) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (STAGES == 2) {
-            wait_vmcnt_barrier<0>();
+            wait_vmcnt_barrier<KSA ? 1 : 0>();   // (KSA: the block's segment load stays in flight)
         } else {
             if (s + STAGES - 2 < num_kb)
                 wait_vmcnt_barrier<(STAGES - 2) * LOADS_PER_STAGE>();
@@ -376,11 +422,17 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
 
     if constexpr (!KT) {
     // Prologue: every slot is free, so the first STAGES stages are issued at once.
+    if constexpr (KSA) {
+        // group 0 whole (wave w < KSA loads segment w) and segment 0 of group 1
+        if (wave < KSA) issue_segment(0, min(wave, KSA - 1), true);
+        issue_block_segment(-1);
+    }
 #pragma unroll
     for (int s = 0; s < STAGES; ++s)
         if (s < num_kb) issue_stage(s, s);
     __builtin_amdgcn_sched_barrier(0);
-    if (num_kb >= STAGES)
+    // (KSA: the group loads are in flight too; wait for all)
+    if (!KSA && num_kb >= STAGES)
         wait_vmcnt_barrier<(STAGES - 1) * LOADS_PER_STAGE>();
     else
         wait_vmcnt_barrier<0>();
@@ -400,6 +452,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     static_assert(SM % 2 == 0, "A fragment double buffer: the next block's first slice goes to buffer 0");
     f32x16 acc[SN];
     for (int kb = 0; kb < num_kb; ++kb) {
+        if constexpr (KSA) issue_block_segment(kb);
         if (!wave_computes) {
             wait_stage(kb + 1);
             issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES);
@@ -562,11 +615,26 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
     const dim3 gdim(static_cast<unsigned>(grid)), bdim(WGM * WGN * 64);
     const bool k_tail = (a.k % kBK) != 0;
+    // K-major SFA scale groups (one 16- or 32-byte load of a row's scales per 4 or 8 K blocks)
+    constexpr bool KSA_OK = STAGES == 2 && !PERSIST && (KIND == kNormal || KIND == kContiguous);
+    const bool kmajor = KSA_OK && a.sfa_sk == 1 && a.sfa_sm % 4 == 0 && (reinterpret_cast<uintptr_t>(a.sfa) & 15) == 0;
+    const int ksa = !kmajor || a.k > kMaxKBlocksKsa * kBK ? 0
+                    : a.k % (8 * kBK) == 0                ? 8
+                    : a.k % (4 * kBK) == 0                ? 4
+                                                          : 0;
 #define DG_PIPE_LAUNCH(OF, HC)                                                                                       \
     do {                                                                                                             \
         if (k_tail)                                                                                                  \
             hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 1, PERSIST>), gdim, \
                                bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
+        else if (ksa == 8)                                                                                           \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST, 0,        \
+                                                          KSA_OK ? 8 : 0>),                                          \
+                               gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                    \
+        else if (ksa == 4)                                                                                           \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST, 0,        \
+                                                          KSA_OK ? 4 : 0>),                                          \
+                               gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                    \
         else                                                                                                         \
             hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST>), gdim, \
                                bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \

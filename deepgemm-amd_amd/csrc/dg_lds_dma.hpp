@@ -40,6 +40,20 @@ __device__ __forceinline__ void dma4_saddr(const uint8_t* base, uint32_t voff, u
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(voff), "s"(base)
                  : "memory", "m0");
 }
+// dma16_saddr with the wave's EXEC mask replaced by `exec_mask` for the one load
+// (0: no lane accesses memory). One asm statement, so the compiler sees no branch
+// (a branch in the middle of an MFMA sequence costs registers); the mask is
+// computed by the caller, and the statement itself only moves EXEC.
+__device__ __forceinline__ void dma16_saddr_masked(uint64_t exec_mask, const uint8_t* base, uint32_t voff,
+                                                   uint32_t lds) {
+    uint64_t saved;
+    asm volatile(
+        "s_mov_b64 %0, exec\n\ts_mov_b64 exec, %4\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\ts_mov_b64 exec, %0"
+        : "=&s"(saved)
+        : "s"(lds), "v"(voff), "s"(base), "s"(exec_mask)
+        : "memory", "m0");
+}
 __device__ __forceinline__ void dma16_vaddr(const void* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src)
                  : "memory", "m0");

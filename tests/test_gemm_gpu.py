@@ -149,9 +149,14 @@ def test_dense_determinism_and_bounds():
     assert bool((big.view(torch.int16)[mask] == SENTINEL).all())
 
 
-def test_mn_major_sfa_equals_k_major():
-    """SFA in the reference's MN-major TMA-aligned layout gives the same bits as K-major SFA."""
-    m, n, k = 130, 256, 1024
+@pytest.mark.parametrize('tile', [None, (2, 256, 256), (2, 256, 192), (2, 128, 256)])
+@pytest.mark.parametrize('m,n,k', [(130, 256, 1024), (300, 520, 2048), (257, 384, 1408), (64, 256, 512),
+                                   (200, 256, 1536), (260, 256, 7168), (200, 384, 4608)])
+def test_mn_major_sfa_equals_k_major(tile, m, n, k):
+    """SFA in the reference's MN-major TMA-aligned layout gives the same bits as K-major SFA.
+    With two-stage tiles, K-major SFA is read through the kernel's scale groups of
+    8 K blocks (K % 1024 == 0) or 4 (K % 512 == 0; K = 1408 keeps the per-stage
+    loads), and each case is checked against the oracle as well."""
     x = gen.dense_inputs(m, n, k, seed=4)
     a_t, b = e4m3(x['qa']), (e4m3(x['qb']), f32(x['sfb']))
     sfa = f32(x['sfa'])
@@ -159,9 +164,18 @@ def test_mn_major_sfa_equals_k_major():
     assert sfa_mn.stride() == (1, deep_gemm.get_tma_aligned_size(m, 4))
     d1 = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
     d2 = torch.empty_like(d1)
-    deep_gemm.fp8_gemm_nt((a_t, sfa), b, d1)
-    deep_gemm.fp8_gemm_nt((a_t, sfa_mn), b, d2)
+    if tile is not None:
+        deep_gemm.set_tile_override(tile[1], tile[2], variant=tile[0])
+    try:
+        deep_gemm.fp8_gemm_nt((a_t, sfa), b, d1)
+        print(deep_gemm.get_last_config(), flush=True)
+        deep_gemm.fp8_gemm_nt((a_t, sfa_mn), b, d2)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
     assert torch.equal(d1.view(torch.int16), d2.view(torch.int16))
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    diff, _ = report(f'sfa layouts {m}x{n}x{k} {tile}', d1.float().cpu().numpy(), ref)
+    assert diff < 1e-3
 
 
 def test_k_zero_and_empty():
