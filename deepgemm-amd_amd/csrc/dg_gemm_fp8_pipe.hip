@@ -666,9 +666,11 @@ void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
 // each group's K) a multiple of 128.
 template <int KIND>
 void launch_1d1d_kind(const Fp8GemmArgs& a, hipStream_t stream) {
-    // 256 x 128 with four waves of 128 x 64: the per-column scales (16 more live
-    // registers per sub-tile column) do not fit the 256 registers of the
-    // eight-wave 256 x 256 tile.
+    // 256 x 128 with eight waves of 64 x 64 (231 registers, two waves per SIMD, so
+    // one wave's promotion, twice the VALU work of the 1D2D recipe's, runs under
+    // the other's MFMAs): the per-column scales (16 more live registers per
+    // sub-tile column) do not fit the 256 registers of the eight-wave 256 x 256
+    // tile.
     constexpr int BM = 256, BN = 128;
     const int num_n_blocks = (a.n + BN - 1) / BN;
     const int num_m_blocks = (a.m + BM - 1) / BM;
@@ -678,8 +680,8 @@ void launch_1d1d_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     DG_CHECK(grid < (int64_t)1 << 31);
     DG_CHECK(a.out_f32 && a.c != nullptr && a.k % kBK == 0);
     const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
-    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, 2, 2, 3, KIND, 1, 1, 0, 0, 1>), dim3((unsigned)grid),
-                       dim3(256), 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, 4, 2, 3, KIND, 1, 1, 0, 0, 1>), dim3((unsigned)grid),
+                       dim3(512), 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
     DG_HIP_CHECK(hipGetLastError());
 }
 
