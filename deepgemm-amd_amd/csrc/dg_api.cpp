@@ -360,12 +360,21 @@ bool is_ue8m0_path(const Operands& o, const Recipe& r) {
 
 // expected_m: the masked layout's per-group row hint (tile choice only), else -1.
 void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int64_t n, int64_t k, int64_t groups,
-              int disable_ue8m0_cast, int zero_padding, hipStream_t stream, int expected_m = -1) {
+              int disable_ue8m0_cast, int zero_padding, hipStream_t stream, int expected_m = -1,
+              const dg_epilogue* ep = nullptr) {
+    // Epilogue classes and alpha exist on the UE8M0 path only, as in the reference
+    // (csrc/apis/gemm.hpp:118-119 for its FP32-scale path); the FP8 stage is a BF16 D
+    // without C (csrc/jit_kernels/impls/epilogue_class.hpp:81-84).
+    if (ep) {
+        DG_CHECK(ep->kind == DG_EPILOGUE_IDENTITY || ep->kind == DG_EPILOGUE_ALPHA || ep->kind == DG_EPILOGUE_FP8_STAGE);
+        if (ep->kind == DG_EPILOGUE_FP8_STAGE) DG_CHECK(o.c == nullptr && o.d.dtype() == DG_BF16);
+    }
     const int align_m = g_mk_alignment.load();
     const bool grouped_b = kind != kNormal;
     const bool grouped_a = kind == kMasked;
 
     if (is_1d2d(o, r)) {
+        DG_CHECK(ep == nullptr && "alpha and epilogue classes need UE8M0 scales");
         // The kernels move K in 16-byte chunks; a partial chunk would pull in the
         // bytes past K of a padded row.
         if (k % 16 != 0) DG_UNSUPPORTED("K must be a multiple of 16 on the FP32-scale FP8 path");
@@ -462,6 +471,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         args.sfb_sn = o.sfb.stride(-2), args.sfb_sk = o.sfb.stride(-1);
         args.sfb_gs = grouped_b ? o.sfb.stride(0) : 0;
         args.sfb_row_shift = r.gran_mn_b == 128 ? 7 : 0;
+        args.alpha = (ep && ep->kind == DG_EPILOGUE_ALPHA) ? ep->alpha : 1.0f;
         // The 256 x 256 pipelined kernel takes packed scale words and K % 128 == 0;
         // everything else runs on the 128 x 128 kernel. A tile override selects
         // the kernel by its variant (1: 128 x 128, 2: pipelined).
@@ -483,6 +493,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
     }
 
     if (is_1d1d(o, r)) {
+        DG_CHECK(ep == nullptr && "alpha and epilogue classes need UE8M0 scales");
         // csrc/jit_kernels/impls/sm90_fp8_gemm_1d1d.hpp:91: FP32 D, accumulating into C
         DG_CHECK(o.c != nullptr && o.d.dtype() == DG_F32);
         if (kind != kNormal) DG_UNSUPPORTED("the 1D1D recipe runs the dense and K-grouped GEMMs only");
@@ -515,7 +526,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
 
 void gemm_nt_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
                   const dg_tensor* d_, const dg_tensor* c, const dg_recipe* recipe, int disable_ue8m0_cast,
-                  hipStream_t stream) {
+                  const dg_epilogue* ep, hipStream_t stream) {
     const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
                d = view(d_, "d");
     // Shape must be [M, K] @ [N, K].T; the gfx950 kernels need K-major operands
@@ -533,13 +544,13 @@ void gemm_nt_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b
     const Recipe r = resolve_recipe(recipe, sfa, sfb);
     check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, -1);
     check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, -1);
-    run_gemm(kNormal, Operands{a, sfa, b, sfb, d, c, nullptr}, r, m, n, k, 1, disable_ue8m0_cast, 0, stream);
+    run_gemm(kNormal, Operands{a, sfa, b, sfb, d, c, nullptr}, r, m, n, k, 1, disable_ue8m0_cast, 0, stream, -1, ep);
 }
 
 void contiguous_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
                      const dg_tensor* d_, const dg_tensor* layout_, const dg_recipe* recipe, int disable_ue8m0_cast,
                      int use_psum_layout, int ensure_zero_padding, int expected_m_for_psum_layout,
-                     hipStream_t stream) {
+                     const dg_epilogue* ep, hipStream_t stream) {
     const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
                d = view(d_, "d"), gl = view(layout_, "grouped_layout");
     // Shape must be [M, K] @ [G, N, K].mT (csrc/apis/gemm.hpp:195-218)
@@ -568,12 +579,12 @@ void contiguous_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor
     check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, -1);
     check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, groups);
     run_gemm(use_psum_layout ? kPsum : kContiguous, Operands{a, sfa, b, sfb, d, nullptr, layout_}, r, m, n, k, groups,
-             disable_ue8m0_cast, use_psum_layout && ensure_zero_padding, stream);
+             disable_ue8m0_cast, use_psum_layout && ensure_zero_padding, stream, -1, ep);
 }
 
 void masked_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
                  const dg_tensor* d_, const dg_tensor* masked_m_, int expected_m, const dg_recipe* recipe,
-                 int disable_ue8m0_cast, hipStream_t stream) {
+                 int disable_ue8m0_cast, const dg_epilogue* ep, hipStream_t stream) {
     const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
                d = view(d_, "d"), mm = view(masked_m_, "masked_m");
     // Shape must be [G, M, K] @ [G, N, K].mT (csrc/apis/gemm.hpp:282-297)
@@ -596,7 +607,7 @@ void masked_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_
     check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, g);
     check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, g);
     run_gemm(kMasked, Operands{a, sfa, b, sfb, d, nullptr, masked_m_}, r, m, n, k, g, disable_ue8m0_cast, 0, stream,
-             expected_m);
+             expected_m, ep);
 }
 
 // ---------------------------------------------------------------- SF layouts
@@ -822,9 +833,9 @@ int dg_shutdown(void) { return guarded([] {}); }
 
 int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b, const dg_tensor* sfb,
                        const dg_tensor* d, const dg_tensor* c, const dg_recipe* recipe, int32_t disable_ue8m0_cast,
-                       void* stream) {
+                       const dg_epilogue* epilogue, void* stream) {
     return guarded([&] {
-        gemm_nt_impl(a, sfa, b, sfb, d, c, recipe, disable_ue8m0_cast, static_cast<hipStream_t>(stream));
+        gemm_nt_impl(a, sfa, b, sfb, d, c, recipe, disable_ue8m0_cast, epilogue, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -832,10 +843,11 @@ int dg_m_grouped_fp8_fp4_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor*
                                             const dg_tensor* sfb, const dg_tensor* d, const dg_tensor* grouped_layout,
                                             const dg_recipe* recipe, int32_t disable_ue8m0_cast,
                                             int32_t use_psum_layout, int32_t ensure_zero_padding,
-                                            int32_t expected_m_for_psum_layout, void* stream) {
+                                            int32_t expected_m_for_psum_layout, const dg_epilogue* epilogue,
+                                            void* stream) {
     return guarded([&] {
         contiguous_impl(a, sfa, b, sfb, d, grouped_layout, recipe, disable_ue8m0_cast, use_psum_layout,
-                        ensure_zero_padding, expected_m_for_psum_layout, static_cast<hipStream_t>(stream));
+                        ensure_zero_padding, expected_m_for_psum_layout, epilogue, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -863,9 +875,9 @@ int dg_k_grouped_fp8_gemm_tn_contiguous(const dg_tensor* a, const dg_tensor* sfa
 int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
                                         const dg_tensor* sfb, const dg_tensor* d, const dg_tensor* masked_m,
                                         int32_t expected_m, const dg_recipe* recipe, int32_t disable_ue8m0_cast,
-                                        void* stream) {
+                                        const dg_epilogue* epilogue, void* stream) {
     return guarded([&] {
-        masked_impl(a, sfa, b, sfb, d, masked_m, expected_m, recipe, disable_ue8m0_cast,
+        masked_impl(a, sfa, b, sfb, d, masked_m, expected_m, recipe, disable_ue8m0_cast, epilogue,
                     static_cast<hipStream_t>(stream));
     });
 }

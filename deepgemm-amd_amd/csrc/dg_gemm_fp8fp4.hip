@@ -221,6 +221,16 @@ fp8_fp4_gemm_kernel(const Fp8Fp4GemmArgs p, const int num_m_blocks, const int nu
         __syncthreads();
     }
 
+    // Alpha epilogue: the product is scaled (one FP32 multiply, never fused with the
+    // addition of C that follows) before C is added.
+    if (p.alpha != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) fin[i][j][e] = __fmul_rn(fin[i][j][e], p.alpha);
+    }
     const int64_t d_goff = (KIND == kMasked) ? (int64_t)t.g * p.d_gs : 0;
 #pragma unroll
     for (int i = 0; i < SM; ++i) {

@@ -316,6 +316,16 @@ fp8_fp4_gemm_pipe_kernel(const Fp8Fp4GemmArgs p, const int num_m_blocks, const i
     // epilogue reuses it).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+    // Alpha epilogue: the product is scaled (one FP32 multiply, never fused with the
+    // addition of C that follows) before C is added.
+    if (p.alpha != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = __fmul_rn(acc[i][j][e], p.alpha);
+    }
     // Row-coalesced epilogue through LDS (dg_epilogue.hpp).
     __syncthreads();
     {

@@ -134,6 +134,7 @@ struct Fp8Fp4GemmArgs {
     int32_t sfa_packed, sfb_packed;   // 1: int32 words of 4 UE8M0 bytes along K
     int32_t gran_k_a, gran_k_b;       // 32 or 128
     int32_t sfb_row_shift;            // SFB row = n >> shift (0, or 7 for 128-row blocks)
+    float alpha;                      // D = C + alpha * (A @ B^T) (1: plain)
     int64_t lda, ldb, ldd, ldc;       // in bytes for a/b, elements for c/d
     int64_t a_gs, b_gs, d_gs, c_gs;   // a/b in bytes, c/d in elements
     int64_t sfa_sm, sfa_sk, sfa_gs;   // in SF elements (floats or int32 words)

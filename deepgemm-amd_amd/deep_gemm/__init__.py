@@ -100,33 +100,95 @@ def get_theoretical_mk_alignment_for_contiguous_layout(expected_m: Optional[int]
 # ------------------------------------------------------------------ epilogues
 
 class _EpilogueNamespace:
-    """Stand-in for the reference's `_C.epilogue` classes: only Identity is implemented."""
+    """The reference's `deep_gemm.epilogue` classes (csrc/apis/epilogue_class.hpp:13-24;
+    semantics csrc/jit_kernels/impls/epilogue_class.hpp:19-124). Identity, Alpha and
+    FP8Quantization run on the UE8M0 (power-of-two scale) path, which is where the
+    reference has them (its FP32-scale path takes none, csrc/apis/gemm.hpp:118-119).
+    BF16StochasticRounding is not provided: its bits are those of NVIDIA's cvt.rs
+    rounding."""
 
-    class Identity:
+    class Epilogue:
         pass
 
-    class Alpha:
-        def __init__(self, *args, **kwargs):
-            raise RuntimeError('Unsupported error: the Alpha epilogue is not provided on gfx950')
+    class Identity(Epilogue):
+        def __init__(self):
+            pass
 
-    class FP8Quantization:
-        def __init__(self, *args, **kwargs):
-            raise RuntimeError('Unsupported error: the FP8Quantization epilogue is not provided on gfx950')
+    class Alpha(Epilogue):
+        """D = C + alpha * (A @ B.T): alpha scales the product, before C is added."""
+        def __init__(self, alpha: float):
+            self.alpha = float(alpha)
 
-    class BF16StochasticRounding:
-        def __init__(self, *args, **kwargs):
-            raise RuntimeError('Unsupported error: the BF16StochasticRounding epilogue is not provided on gfx950')
+    class FP8Quantization(Epilogue):
+        """E4M3 D with per-row, per-32-column UE8M0 scales packed into the int32 words
+        of `sfd` (MN-major, [M, ceil(N / 128)]): bitwise a BF16 D followed by
+        per_token_cast_to_fp8(d, use_ue8m0=True, gran_k=32), which is how the reference
+        defines it (deep_gemm/include/deep_gemm/epilogue/operators.cuh:65-69)."""
+        def __init__(self, sfd: torch.Tensor):
+            self.sfd = sfd
+
+    class BF16StochasticRounding(Epilogue):
+        def __init__(self):
+            pass
 
 
 epilogue = _EpilogueNamespace()
 
 
-def _check_epilogue(ep, alpha=None):
-    if ep is not None and not isinstance(ep, _EpilogueNamespace.Identity):
-        raise RuntimeError('Assertion error (gemm.hpp): epilogue_class == nullptr and "Custom epilogues are not provided"')
+def _resolve_epilogue(ep, alpha=None):
+    """(dg_epilogue or None, FP8Quantization or None): the reference's
+    resolve_epilogue_class (csrc/jit_kernels/impls/epilogue_class.hpp:111-124)."""
+    if (ep is not None) + (alpha is not None) > 1:
+        raise RuntimeError('Assertion error (epilogue_class.hpp:116): (epilogue_class != nullptr) + '
+                           'alpha.has_value() + sfd.has_value() <= 1 and "The epilogue class, `alpha` and the '
+                           'FP8 output pair are exclusive"')
     if alpha is not None:
-        # The reference's FP32-scale (SM90) path rejects alpha the same way (csrc/apis/gemm.hpp:118).
-        raise RuntimeError('Assertion error (gemm.hpp:118): not alpha.has_value() and "FP8 GEMM alpha is not provided"')
+        ep = _EpilogueNamespace.Alpha(alpha)
+    if ep is None:
+        return None, None
+    if isinstance(ep, _EpilogueNamespace.BF16StochasticRounding):
+        raise RuntimeError('Unsupported error: the BF16StochasticRounding epilogue (NVIDIA cvt.rs) is not provided '
+                           'on gfx950')
+    if isinstance(ep, _EpilogueNamespace.Alpha):
+        return _ffi.DgEpilogue(_ffi.EPILOGUE_ALPHA, ep.alpha), None
+    if isinstance(ep, _EpilogueNamespace.FP8Quantization):
+        return _ffi.DgEpilogue(_ffi.EPILOGUE_FP8_STAGE, 1.0), ep
+    if isinstance(ep, _EpilogueNamespace.Identity):
+        return _ffi.DgEpilogue(_ffi.EPILOGUE_IDENTITY, 1.0), None
+    raise TypeError('epilogue must be one of deep_gemm.epilogue.Identity / Alpha / FP8Quantization')
+
+
+def _check_epilogue(ep, alpha=None):
+    """The FP32-scale K-grouped path takes no epilogue (reference csrc/apis/gemm.hpp:118-119)."""
+    if ep is not None or alpha is not None:
+        raise RuntimeError('Assertion error (gemm.hpp:118): not alpha.has_value() and epilogue_class == nullptr '
+                           'and "alpha and epilogue classes need UE8M0 scales"')
+
+
+def _fp8_quantized_output(d: torch.Tensor, c, k: int, fp8q, run_bf16) -> None:
+    """FP8Quantization: run the GEMM into a BF16 stage, then cast it per 32 columns with
+    UE8M0 scales into d and fp8q.sfd (the reference's definition of the fused form)."""
+    if c is not None or d.dtype != torch.float8_e4m3fn:
+        raise RuntimeError('Assertion error (epilogue_class.hpp:82): not c.has_value() and d.scalar_type() == '
+                           'torch::kFloat8_e4m3fn and "FP8 quantization requires a direct E4M3 output"')
+    if d.dim() != 2:
+        raise RuntimeError('Unsupported error: the FP8Quantization epilogue takes a 2-D D here')
+    m, n = d.shape
+    sfd = fp8q.sfd
+    words = (((n + 31) // 32) + 3) // 4
+    if sfd.dtype != torch.int32 or tuple(sfd.shape) != (m, words):
+        raise RuntimeError(f'Assertion error: sfd must be int32 [{m}, {words}] (packed UE8M0 words, MN-major)')
+    if m == 0 or n == 0:
+        return
+    if k == 0:   # a zero D dequantizes to zero whatever the SF (reference csrc/apis/gemm.hpp:38-45)
+        d.zero_()
+        sfd.zero_()
+        return
+    stage = torch.empty((m, n), dtype=torch.bfloat16, device=d.device)
+    run_bf16(stage)
+    q, sf = per_token_cast_to_fp8(stage, use_ue8m0=True, gran_k=32)
+    d.copy_(q)
+    sfd.copy_(get_mn_major_tma_aligned_packed_ue8m0_tensor(sf))
 
 
 def _pair(x, name):
@@ -142,15 +204,23 @@ def fp8_fp4_gemm_nt(a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.Tensor,
                     recipe_a: Optional[Tuple[int, int]] = None, recipe_b: Optional[Tuple[int, int]] = None,
                     compiled_dims: str = 'nk', disable_ue8m0_cast: bool = False, alpha: Optional[float] = None,
                     epilogue=None) -> None:
-    """D = C + A @ B.T with block scales (reference csrc/apis/gemm.hpp:78-133)."""
-    _check_epilogue(epilogue, alpha)
+    """D = C + A @ B.T with block scales (reference csrc/apis/gemm.hpp:78-133); `alpha`
+    and `epilogue` as the reference's UE8M0 path takes them (see `epilogue`)."""
+    ep, fp8q = _resolve_epilogue(epilogue, alpha)
     a_t, sfa = _pair(a, 'a')
     b_t, sfb = _pair(b, 'b')
-    da, dsa, db, dsb, dd = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d)
+    da, dsa, db, dsb = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb)
     dc = _desc(c) if c is not None else None
     r = _ffi.recipe_struct(recipe, recipe_a, recipe_b)
-    _check(_lib.dg_fp8_fp4_gemm_nt(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dc), _ref(r),
-                                   int(bool(disable_ue8m0_cast)), _ffi.stream_of(d)))
+
+    def run(out):
+        dd = _desc(out)
+        _check(_lib.dg_fp8_fp4_gemm_nt(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dc), _ref(r),
+                                       int(bool(disable_ue8m0_cast)), _ref(ep), _ffi.stream_of(out)))
+    if fp8q is not None:
+        _fp8_quantized_output(d, c, a_t.shape[-1], fp8q, run)
+    else:
+        run(d)
 
 
 def fp8_fp4_gemm_nn(a, b, d, c=None, recipe=None, recipe_a=None, recipe_b=None, compiled_dims='nk',
@@ -181,8 +251,10 @@ def m_grouped_fp8_fp4_gemm_nt_contiguous(a, b, d: torch.Tensor, grouped_layout: 
                                          expected_m_for_psum_layout: Optional[int] = None, epilogue=None) -> None:
     """D[r] = A[r] @ B[e(r)].T over 128-row-aligned expert segments
     (reference csrc/apis/gemm.hpp:181-250). Rows with grouped_layout == -1 are
-    left untouched."""
-    _check_epilogue(epilogue)
+    left untouched. `epilogue`: Identity or Alpha on the UE8M0 path."""
+    ep, fp8q = _resolve_epilogue(epilogue)
+    if fp8q is not None:
+        raise RuntimeError('Unsupported error: the FP8Quantization epilogue takes the dense GEMM here')
     a_t, sfa = _pair(a, 'a')
     b_t, sfb = _pair(b, 'b')
     da, dsa, db, dsb, dd, dl = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d), _desc(grouped_layout)
@@ -190,7 +262,8 @@ def m_grouped_fp8_fp4_gemm_nt_contiguous(a, b, d: torch.Tensor, grouped_layout: 
     _check(_lib.dg_m_grouped_fp8_fp4_gemm_nt_contiguous(
         _ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dl), _ref(r), int(bool(disable_ue8m0_cast)),
         int(bool(use_psum_layout)), int(bool(ensure_zero_padding)),
-        -1 if expected_m_for_psum_layout is None else int(expected_m_for_psum_layout), _ffi.stream_of(d)))
+        -1 if expected_m_for_psum_layout is None else int(expected_m_for_psum_layout), _ref(ep),
+        _ffi.stream_of(d)))
 
 
 def m_grouped_fp8_fp4_gemm_nn_contiguous(a, b, d, grouped_layout, recipe=None, recipe_a=None, recipe_b=None,
@@ -206,15 +279,18 @@ def m_grouped_fp8_fp4_gemm_nt_masked(a, b, d: torch.Tensor, masked_m: torch.Tens
                                      recipe=None, recipe_a=None, recipe_b=None, compiled_dims: str = 'nk',
                                      disable_ue8m0_cast: bool = False, epilogue=None) -> None:
     """D[g, r] = A[g, r] @ B[g].T for r < masked_m[g] (reference
-    csrc/apis/gemm.hpp:269-318). Rows >= masked_m[g] are left untouched."""
-    _check_epilogue(epilogue)
+    csrc/apis/gemm.hpp:269-318). Rows >= masked_m[g] are left untouched. `epilogue`:
+    Identity or Alpha on the UE8M0 path."""
+    ep, fp8q = _resolve_epilogue(epilogue)
+    if fp8q is not None:
+        raise RuntimeError('Unsupported error: the FP8Quantization epilogue takes the dense GEMM here')
     a_t, sfa = _pair(a, 'a')
     b_t, sfb = _pair(b, 'b')
     da, dsa, db, dsb, dd, dm = _desc(a_t), _desc(sfa), _desc(b_t), _desc(sfb), _desc(d), _desc(masked_m)
     r = _ffi.recipe_struct(recipe, recipe_a, recipe_b)
     _check(_lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(
         _ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dm), int(expected_m), _ref(r),
-        int(bool(disable_ue8m0_cast)), _ffi.stream_of(d)))
+        int(bool(disable_ue8m0_cast)), _ref(ep), _ffi.stream_of(d)))
 
 
 def _k_grouped(entry, a, b, d, ks_cpu, grouped_layout, c, recipe, use_psum_layout, epilogue):

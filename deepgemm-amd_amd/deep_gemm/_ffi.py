@@ -52,9 +52,17 @@ class DgRecipe(ctypes.Structure):
                 ('recipe_b', ctypes.c_int32 * 2)]
 
 
+class DgEpilogue(ctypes.Structure):
+    _fields_ = [('kind', ctypes.c_int32),
+                ('alpha', ctypes.c_float)]
+
+
+EPILOGUE_IDENTITY, EPILOGUE_ALPHA, EPILOGUE_FP8_STAGE = 0, 1, 2
+
 _P = ctypes.POINTER
 _T = _P(DgTensor)
 _R = _P(DgRecipe)
+_E = _P(DgEpilogue)
 _I = ctypes.c_int32
 _V = ctypes.c_void_p
 
@@ -64,9 +72,9 @@ SIGNATURES = {
     'dg_version': (ctypes.c_char_p, []),
     'dg_init': (_I, []),
     'dg_shutdown': (_I, []),
-    'dg_fp8_fp4_gemm_nt': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _V]),
-    'dg_m_grouped_fp8_fp4_gemm_nt_contiguous': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _I, _I, _I, _V]),
-    'dg_m_grouped_fp8_fp4_gemm_nt_masked': (_I, [_T, _T, _T, _T, _T, _T, _I, _R, _I, _V]),
+    'dg_fp8_fp4_gemm_nt': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _E, _V]),
+    'dg_m_grouped_fp8_fp4_gemm_nt_contiguous': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _I, _I, _I, _E, _V]),
+    'dg_m_grouped_fp8_fp4_gemm_nt_masked': (_I, [_T, _T, _T, _T, _T, _T, _I, _R, _I, _E, _V]),
     'dg_get_tma_aligned_size': (_I, [_I, _I, _P(_I)]),
     'dg_get_mn_major_tma_aligned_tensor': (_I, [_T, _T, _V]),
     'dg_get_mn_major_tma_aligned_packed_ue8m0_tensor': (_I, [_T, _T, _V]),

@@ -74,6 +74,27 @@ typedef struct dg_recipe {
     int32_t recipe_b[2];
 } dg_recipe;
 
+/* GEMM epilogue of the UE8M0 (power-of-two scale) path: the reference's
+ * `epilogue` / `alpha` arguments (csrc/jit_kernels/impls/epilogue_class.hpp:
+ * 19-124, resolved by resolve_epilogue_class :111-124). NULL means neither was
+ * given. The FP32-scale path takes none (csrc/apis/gemm.hpp:118-119).
+ *   DG_EPILOGUE_IDENTITY  store the result as is
+ *   DG_EPILOGUE_ALPHA     D = C + alpha * (A @ B^T): alpha scales the product
+ *                         (an FP32 multiply) before C is added
+ *                         (deep_gemm/include/deep_gemm/epilogue/operators.cuh:17-30)
+ *   DG_EPILOGUE_FP8_STAGE the BF16 D of an FP8Quantization epilogue: D must be
+ *                         BF16 and C NULL; the caller casts it with
+ *                         dg_per_token_cast_to_fp8 (gran_k 32, UE8M0), which the
+ *                         reference defines as bitwise equal to its fused form
+ *                         (deep_gemm/include/deep_gemm/epilogue/operators.cuh:65-69). */
+#define DG_EPILOGUE_IDENTITY 0
+#define DG_EPILOGUE_ALPHA 1
+#define DG_EPILOGUE_FP8_STAGE 2
+typedef struct dg_epilogue {
+    int32_t kind;
+    float alpha;
+} dg_epilogue;
+
 /* ---------------------------------------------------------------- lifecycle */
 
 /* Thread-local message of the last failed call on this thread ("" if none). */
@@ -105,12 +126,14 @@ int dg_shutdown(void);
  * (1,128,128) recipe always take the FP32-scale path. FP32 SFs of the (1,1,128)
  * recipe (sfb [N, ceil(K/128)], one scale per B row: the reference's SM90
  * "1D1D" weight-gradient kernel, csrc/apis/gemm.hpp:119-122) need an FP32 d
- * and a c (csrc/jit_kernels/impls/sm90_fp8_gemm_1d1d.hpp:91), and K % 128 == 0. */
+ * and a c (csrc/jit_kernels/impls/sm90_fp8_gemm_1d1d.hpp:91), and K % 128 == 0.
+ * epilogue: see dg_epilogue (UE8M0 scale path only). */
 int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa,
                        const dg_tensor* b, const dg_tensor* sfb,
                        const dg_tensor* d, const dg_tensor* c,
                        const dg_recipe* recipe,
                        int32_t disable_ue8m0_cast,
+                       const dg_epilogue* epilogue,
                        void* stream);
 
 /* M-grouped contiguous GEMM (prefill MoE).
@@ -132,6 +155,7 @@ int dg_m_grouped_fp8_fp4_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor*
                                             int32_t use_psum_layout,
                                             int32_t ensure_zero_padding,
                                             int32_t expected_m_for_psum_layout,
+                                            const dg_epilogue* epilogue,
                                             void* stream);
 
 /* M-grouped masked GEMM (decode MoE).
@@ -147,6 +171,7 @@ int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa
                                         int32_t expected_m,
                                         const dg_recipe* recipe,
                                         int32_t disable_ue8m0_cast,
+                                        const dg_epilogue* epilogue,
                                         void* stream);
 
 /* K-grouped GEMM (weight gradients of MoE experts).

@@ -82,10 +82,11 @@ def fake(shape, dtype, strides=None, addr=0x10000000, device=0):
     return t
 
 
-def call_nt(a, sfa, b, sfb, d, c=None, recipe=None, disable=0):
+def call_nt(a, sfa, b, sfb, d, c=None, recipe=None, disable=0, ep=None):
     st = _ffi.lib.dg_fp8_fp4_gemm_nt(ctypes.byref(a), ctypes.byref(sfa), ctypes.byref(b), ctypes.byref(sfb),
                                     ctypes.byref(d), ctypes.byref(c) if c else None,
-                                    ctypes.byref(recipe) if recipe else None, disable, None)
+                                    ctypes.byref(recipe) if recipe else None, disable,
+                                    ctypes.byref(ep) if ep else None, None)
     return st, _ffi.lib.dg_last_error().decode()
 
 
@@ -231,7 +232,7 @@ def test_grouped_validation():
     d = fake((m, n), _ffi.DG_BF16)
     idx = fake((m - 1,), _ffi.DG_I32)
     st = _ffi.lib.dg_m_grouped_fp8_fp4_gemm_nt_contiguous(*(ctypes.byref(x) for x in (a, sfa, b, sfb, d, idx)),
-                                                          None, 0, 0, 1, -1, None)
+                                                          None, 0, 0, 1, -1, None, None)
     assert st == _ffi.DG_ERR_INVALID and 'gl.size(0) == m' in _ffi.lib.dg_last_error().decode()
     # masked: masked_m length must equal G
     a3 = fake((g, 256, k), _ffi.DG_E4M3)
@@ -239,12 +240,12 @@ def test_grouped_validation():
     d3 = fake((g, 256, n), _ffi.DG_BF16)
     mm = fake((g + 1,), _ffi.DG_I32)
     st = _ffi.lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(*(ctypes.byref(x) for x in (a3, sfa3, b, sfb, d3, mm)),
-                                                      128, None, 0, None)
+                                                      128, None, 0, None, None)
     assert st == _ffi.DG_ERR_INVALID and 'g == g___' in _ffi.lib.dg_last_error().decode()
     # expected_m must be positive
     mm = fake((g,), _ffi.DG_I32)
     st = _ffi.lib.dg_m_grouped_fp8_fp4_gemm_nt_masked(*(ctypes.byref(x) for x in (a3, sfa3, b, sfb, d3, mm)),
-                                                      0, None, 0, None)
+                                                      0, None, 0, None, None)
     assert st == _ffi.DG_ERR_INVALID and 'expected_m > 0' in _ffi.lib.dg_last_error().decode()
 
 
@@ -270,7 +271,45 @@ def test_python_shim_errors():
     s = torch.ones((128, 2))
     with pytest.raises(RuntimeError, match=r'Assertion error \(dg_api\.cpp:\d+\)'):
         deep_gemm.fp8_gemm_nt((x, s), (x, torch.ones((1, 2))), torch.empty((128, 128), dtype=torch.bfloat16))
-    with pytest.raises(RuntimeError, match='alpha'):
+    # (alpha reaches the library, whose device checks come first for host tensors)
+    with pytest.raises(RuntimeError, match=r'Assertion error \(dg_api\.cpp:\d+\)'):
         deep_gemm.fp8_gemm_nt((x, s), (x, s), torch.empty((128, 128)), alpha=2.0)
-    with pytest.raises(RuntimeError, match='epilogue'):
+    with pytest.raises(TypeError, match='epilogue'):
         deep_gemm.fp8_gemm_nt((x, s), (x, s), torch.empty((128, 128)), epilogue=object())
+
+
+def test_epilogue_host_checks():
+    """alpha / epilogue classes exist on the UE8M0 path only (reference
+    csrc/apis/gemm.hpp:118-119 for the FP32-scale path); the FP8 stage is a BF16 D
+    without C; unknown kinds are rejected. All checks run before any launch."""
+    a, sfa, b, sfb, d = good_dense()
+    st, msg = call_nt(a, sfa, b, sfb, d, ep=_ffi.DgEpilogue(_ffi.EPILOGUE_ALPHA, 2.0))
+    assert st == _ffi.DG_ERR_INVALID and 'need UE8M0 scales' in msg, msg
+    st, msg = call_nt(a, sfa, b, sfb, d, ep=_ffi.DgEpilogue(_ffi.EPILOGUE_IDENTITY, 1.0))
+    assert st == _ffi.DG_ERR_INVALID and 'need UE8M0 scales' in msg, msg
+    st, msg = call_nt(a, sfa, b, sfb, d, ep=_ffi.DgEpilogue(7, 1.0))
+    assert st == _ffi.DG_ERR_INVALID and 'DG_EPILOGUE_IDENTITY' in msg, msg
+    c = fake((256, 512), _ffi.DG_BF16)
+    st, msg = call_nt(a, sfa, b, sfb, d, c=c, ep=_ffi.DgEpilogue(_ffi.EPILOGUE_FP8_STAGE, 1.0))
+    assert st == _ffi.DG_ERR_INVALID and 'o.c == nullptr' in msg, msg
+
+
+def test_epilogue_python_resolution():
+    """The Python resolution mirrors resolve_epilogue_class
+    (csrc/jit_kernels/impls/epilogue_class.hpp:111-124) before any device work."""
+    import torch
+    import deep_gemm
+    ep = deep_gemm.epilogue
+    a = (torch.zeros(4, 128, dtype=torch.float8_e4m3fn), torch.zeros(4, 1, dtype=torch.int32))
+    b = (torch.zeros(4, 128, dtype=torch.float8_e4m3fn), torch.zeros(4, 1, dtype=torch.int32))
+    d = torch.zeros(4, 4, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='exclusive'):
+        deep_gemm.fp8_fp4_gemm_nt(a, b, d, alpha=2.0, epilogue=ep.Identity())
+    with pytest.raises(RuntimeError, match='StochasticRounding'):
+        deep_gemm.fp8_fp4_gemm_nt(a, b, d, epilogue=ep.BF16StochasticRounding())
+    with pytest.raises(RuntimeError, match='direct E4M3 output'):
+        deep_gemm.fp8_fp4_gemm_nt(a, b, d, epilogue=ep.FP8Quantization(torch.zeros(4, 1, dtype=torch.int32)))
+    with pytest.raises(RuntimeError, match='need UE8M0 scales'):
+        deep_gemm.k_grouped_fp8_gemm_nt_contiguous(a, b, d, [128], torch.zeros(1, dtype=torch.int32),
+                                                   epilogue=ep.Identity())
+    assert isinstance(ep.Alpha(0.5), ep.Epilogue) and ep.Alpha(0.5).alpha == 0.5
