@@ -727,3 +727,70 @@ def test_fp8_fp4_masked_vs_oracle():
     diff, _ = report('fp8xfp4 masked', out[valid], ref[valid])
     assert diff < 1e-5
     assert bool((d.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
+
+
+def _pad_packed_k(sf, padding=4):
+    """Packed MN-major SF words with a K pitch padding words longer than the aligned
+    MN, the padding poisoned with -1 (UE8M0 NaN bytes): the reference's
+    add_sf_k_padding (tests/utils.py:41-50), which exposes reads that assume a
+    compact pitch."""
+    mn = sf.size(-2)
+    pitch = (mn + 3) // 4 * 4 + padding
+    storage = sf.new_full((sf.numel() // mn, pitch), -1)
+    return storage.as_strided(sf.shape, (1, pitch)).copy_(sf)
+
+
+@pytest.mark.parametrize('m,n,k', [(256, 384, 1024), (300, 520, 640)])
+def test_ue8m0_packed_sf_k_pitch(m, n, k):
+    """Packed SFs with a padded K pitch give the same bits on both UE8M0 kernels
+    (the reference's 'packed SF K-stride' check, tests/test_fp8_fp4.py:86-97)."""
+    qa, sfa, _ = _ue8m0_quant(gen.randn_bf16((m, k), 71), False, 128)
+    qb, sfb, _ = _ue8m0_quant(gen.randn_bf16((n, k), 72), True, 32)
+    a = (e4m3(qa), _packed(sfa))
+    b = (gen.to_dev(qb, torch.int8), _packed(sfb))
+    a_p = (a[0], _pad_packed_k(a[1]))
+    b_p = (b[0], _pad_packed_k(b[1]))
+    assert a_p[1].stride(-1) > a[1].stride(-1)
+
+    def call(x, y):
+        d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        deep_gemm.fp8_fp4_gemm_nt(x, y, d, recipe_a=(1, 128), recipe_b=(1, 32))
+        torch.cuda.synchronize()
+        return d
+
+    (c0, c1), _ = _run_both_kernels(lambda: call(a, b))
+    (p0, p1), _ = _run_both_kernels(lambda: call(a_p, b_p))
+    assert torch.equal(c0.view(torch.int16), p0.view(torch.int16))
+    assert torch.equal(c1.view(torch.int16), p1.view(torch.int16))
+
+
+def test_fp4_equals_converted_fp8():
+    """E2M1 operands and their exact E4M3 conversion (same scales) give the same GEMM
+    up to rounding (reference tests/test_fp8_fp4.py:98-103, whose bar is 1e-14 for
+    NVIDIA's UMMA). The gfx950 matrix core sums E2M1 and E4M3 operands in different
+    internal orders, so some FP32 results differ in their last bits and a few BF16
+    outputs round the other way: measured calc_diff 1.1e-11 at this shape (13 of
+    131072 outputs). The bar here is 1e-9, at most 1% of the outputs may differ,
+    and no difference may exceed half a BF16 step at the output's scale."""
+    from oracle import fp8 as ofp8
+    m, n, k = 256, 512, 1024
+    qa, sfa, _ = _ue8m0_quant(gen.randn_bf16((m, k), 81), False, 128)
+    qb, sfb, _ = _ue8m0_quant(gen.randn_bf16((n, k), 82), True, 32)
+    qb8 = ofp8.e4m3_encode(ofp8.e2m1_decode(ofp8.e2m1_unpack(qb)))
+    assert np.array_equal(ofp8.e4m3_decode(qb8), ofp8.e2m1_decode(ofp8.e2m1_unpack(qb)))   # exact
+    a = (e4m3(qa), _packed(sfa))
+    outs = []
+    for bq in (gen.to_dev(qb, torch.int8), e4m3(qb8)):
+        d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        deep_gemm.fp8_fp4_gemm_nt(a, (bq, _packed(sfb)), d, recipe_a=(1, 128), recipe_b=(1, 32))
+        torch.cuda.synchronize()
+        outs.append(d.float().cpu().numpy())
+    diff = ogemm.calc_diff(outs[0], outs[1])
+    neq = outs[0] != outs[1]
+    worst = np.abs(outs[0] - outs[1]).max()
+    scale = np.abs(outs[0]).max()
+    print(f'fp4 vs converted fp8 calc_diff={diff:.3e}, {neq.sum()} of {neq.size} outputs differ, '
+          f'max difference {worst:.3e} (output scale {scale:.3e})', flush=True)
+    assert diff < 1e-9
+    assert neq.mean() < 0.01
+    assert worst <= 2 ** -9 * scale
