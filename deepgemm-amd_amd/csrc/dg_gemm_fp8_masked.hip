@@ -92,11 +92,14 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
     using S = StreamShape<NW>;
     constexpr int ROWS = NRT * 32;
     constexpr int A_SEGS = ROWS / 8;                        // 1 KB (8-row) wave loads of A per stage
-    constexpr int A_INSTR = (A_SEGS + NW - 1) / NW;         // per wave; surplus loads repeat the last segment
-    constexpr int SA_SEGS = (ROWS + 63) / 64;               // 256 B SFA loads per stage (one per wave, clamped)
+    constexpr int SA_SEGS = (ROWS + 63) / 64;               // 256 B (64-row) SFA loads per stage
+    // A stage loads, one list: the A segments, then the SFA segments; load i of
+    // wave w is entry i * NW + w (past the end: the last entry again), so every
+    // wave issues LA loads and none repeats another's unless the list runs short.
+    constexpr int A_LOADS = A_SEGS + SA_SEGS;
+    constexpr int LA = (A_LOADS + NW - 1) / NW;
     constexpr int A_STAGE = ROWS * kBK + SA_SEGS * 256;
     constexpr int SA = (kLds - S::B_RING) / A_STAGE > 4 ? 4 : (kLds - S::B_RING) / A_STAGE;
-    constexpr int LA = A_INSTR + 1;
     constexpr int LB = S::LB;
     // At the end of block kb, A(kb + 1) and B(kb + 1) must be complete; the loads
     // issued after the later of them are B(kb + 2) (two A stages) or all of
@@ -129,24 +132,33 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
     const uint8_t* __restrict__ a_p = p.a + (int64_t)g * p.a_gs + (int64_t)r0 * p.lda;
     const float* __restrict__ sa_p = p.sfa + (int64_t)g * p.sfa_gs + (int64_t)r0 * p.sfa_sm;
 
-    // Per-lane offsets of the A stage loads: rows past a_rows repeat the last
-    // valid one, whose outputs are never stored.
-    uint32_t voff_a[A_INSTR];
+    // Per-lane offsets of the wave's A stage loads (entry e = i * NW + wave of the
+    // list): rows past a_rows repeat the last valid one, whose outputs are never
+    // stored.
+    uint32_t voff_a[LA];
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i) {
-        const int row = min(i * NW + wave, A_SEGS - 1) * 8 + rs;
-        voff_a[i] = (uint32_t)min(row, a_rows - 1) * (uint32_t)p.lda + ((pc ^ swz_g(row)) << 4);
+    for (int i = 0; i < LA; ++i) {
+        const int e = min(i * NW + wave, A_LOADS - 1);
+        if (e < A_SEGS) {
+            const int row = e * 8 + rs;
+            voff_a[i] = (uint32_t)min(row, a_rows - 1) * (uint32_t)p.lda + ((pc ^ swz_g(row)) << 4);
+        } else {
+            voff_a[i] = (uint32_t)(min((e - A_SEGS) * 64 + lane, a_rows - 1) * p.sfa_sm) * 4u;
+        }
     }
-    const int sa_seg = min(wave, SA_SEGS - 1);
-    const uint32_t voff_sa = (uint32_t)(min(sa_seg * 64 + lane, a_rows - 1) * p.sfa_sm) * 4u;
     auto issue_a = [&](int kb, int st) {
         kb = min(kb, num_kb - 1);   // past the end: reload the last block into the free slot
         const uint32_t lds = a_ring + st * A_STAGE;
         const uint8_t* base = a_p + (int64_t)kb * kBK;
+        const uint8_t* sa_kb = reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk);
 #pragma unroll
-        for (int i = 0; i < A_INSTR; ++i) dma16_saddr(base, voff_a[i], lds + min(i * NW + wave, A_SEGS - 1) * 1024);
-        dma4_saddr(reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk), voff_sa,
-                   lds + ROWS * kBK + sa_seg * 256);
+        for (int i = 0; i < LA; ++i) {
+            const int e = min(i * NW + wave, A_LOADS - 1);   // wave-uniform
+            if (e < A_SEGS)
+                dma16_saddr(base, voff_a[i], lds + e * 1024);
+            else
+                dma4_saddr(sa_kb, voff_a[i], lds + ROWS * kBK + (e - A_SEGS) * 256);
+        }
     };
     auto issue_b = [&](int kb, int st) { S::issue(b_t, voff_b, num_kb, kb, st, wave, smem_lds); };
     // The wave's SFB column (its 32 columns lie in one 128-row group), read with
