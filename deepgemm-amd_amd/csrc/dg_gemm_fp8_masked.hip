@@ -99,7 +99,12 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
     constexpr int A_LOADS = A_SEGS + SA_SEGS;
     constexpr int LA = (A_LOADS + NW - 1) / NW;
     constexpr int A_STAGE = ROWS * kBK + SA_SEGS * 256;
-    constexpr int SA = (kLds - S::B_RING) / A_STAGE > 4 ? 4 : (kLds - S::B_RING) / A_STAGE;
+    // A ring depth: as many stages as fit, at most 4, except with 8 waves
+    // (256-column tiles), where 2 measured faster than 3 (4096 x 7168: 113 against
+    // 117 us; fewer A loads in flight leave the load path to the B stream), while
+    // with 7 waves (7168 x 2048) 3 stay 1.5% faster than 2.
+    constexpr int SA_FIT = (kLds - S::B_RING) / A_STAGE > 4 ? 4 : (kLds - S::B_RING) / A_STAGE;
+    constexpr int SA = NW == 8 ? (SA_FIT < 2 ? SA_FIT : 2) : SA_FIT;
     constexpr int LB = S::LB;
     // At the end of block kb, A(kb + 1) and B(kb + 1) must be complete; the loads
     // issued after the later of them are B(kb + 2) (two A stages) or all of
