@@ -52,6 +52,8 @@ def parse():
     ap.add_argument('--workload', default='dense',
                     choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-extras', action='store_true',
+                    help='default workload only: skip the per-launch summaries of the other configurations')
     ap.add_argument('--rotate', type=int, default=8, help='rotating buffer sets per launch')
     ap.add_argument('--eager', action='store_true', help='launch from Python instead of replaying HIP graphs')
     ap.add_argument('--cpu-sample-m', type=int, default=512)
@@ -100,42 +102,31 @@ def _quant_b(n, k, gen, dev):
     return deep_gemm.per_block_cast_to_fp8(x, use_ue8m0=False)
 
 
-def make_dense(acc: bool):
+# Operand builders: the exact seeded inputs of each configuration. The
+# full-size parity tests (tests/test_configs_gpu.py) build their inputs through
+# these same functions, so the bench workloads are the tested workloads.
+
+def dense_operands(acc: bool, dev='cuda:0'):
+    """Config 2: M = 4096 over DENSE_NK. A 1x128 and B 128x128 FP32-scale e4m3
+    (the product quantizers, on the device); with `acc`, an FP32 C = 32 randn."""
     import torch
-    import deep_gemm
-    dev = torch.device('cuda:0')
     gen = torch.Generator().manual_seed(0)
     m = 4096
-    launches = []
+    out = []
     for n, k in DENSE_NK:
         a = _quant_a(m, k, gen, dev)
         b = _quant_b(n, k, gen, dev)
-        if acc:
-            d = (torch.randn((m, n), generator=gen) * 32).to(dev)
-
-            def mk(a=a, b=b, d=d):
-                a2, b2, d2 = _twin(a), _twin(b), _twin(d)
-                return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2, c=d2)
-            out_bytes = 8 * m * n
-        else:
-            def mk(a=a, b=b, m=m, n=n):
-                a2, b2 = _twin(a), _twin(b)
-                d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-                return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2)
-            out_bytes = 2 * m * n
-        nbytes = m * k + n * k + 4 * m * ((k + 127) // 128) + 4 * ((n + 127) // 128) * ((k + 127) // 128) + out_bytes
-        launches.append(Launch(f'n{n}_k{k}', mk, 2 * m * n * k, nbytes))
-    cfg = {'workload': 'fp8_gemm_nt M=4096 DeepSeek-V3 (N,K) sweep' + (' FP32 C-accumulate' if acc else ''),
-           'm': m, 'nk': DENSE_NK, 'out': 'f32 (D=C+AB^T)' if acc else 'bf16',
-           'recipe': '1x128 A / 128x128 B FP32 scales'}
-    return launches, cfg, 'mfma'
+        c = (torch.randn((m, n), generator=gen) * 32).to(dev) if acc else None
+        out.append(dict(name=f'n{n}_k{k}', m=m, n=n, k=k, a=a, b=b, c=c))
+    return out
 
 
-def make_contiguous():
+def contiguous_operands(dev='cuda:0'):
+    """Config 3: 8 experts, 32768 tokens ~ Multinomial(Dirichlet(1)), segments
+    padded to the M alignment with m_indices = -1 and zero A rows."""
     import numpy as np
     import torch
     import deep_gemm
-    dev = torch.device('cuda:0')
     gen = torch.Generator().manual_seed(0)
     rng = np.random.default_rng(0)
     g, total = 8, 32768
@@ -143,44 +134,36 @@ def make_contiguous():
     align = deep_gemm.get_mk_alignment_for_contiguous_layout()
     aligned = [(int(x) + align - 1) // align * align for x in ms]
     m_pad = sum(aligned)
-    idx = torch.full((m_pad,), -1, dtype=torch.int32)
+    idx_h = torch.full((m_pad,), -1, dtype=torch.int32)
     s = 0
     for i, (mi, ai) in enumerate(zip(ms, aligned)):
-        idx[s:s + int(mi)] = i
+        idx_h[s:s + int(mi)] = i
         s += ai
-    idx = idx.to(dev)
-    launches = []
+    idx = idx_h.to(dev)
+    shapes = []
     for n, k in [(4096, 7168), (7168, 2048)]:
         x = torch.randn((m_pad, k), generator=gen).bfloat16()
-        x[idx.cpu() < 0] = 0
+        x[idx_h < 0] = 0
         a = deep_gemm.per_token_cast_to_fp8(x.to(dev), use_ue8m0=False)
         bq = torch.empty((g, n, k), dtype=torch.float8_e4m3fn, device=dev)
         bs = torch.empty((g, (n + 127) // 128, (k + 127) // 128), device=dev)
         for i in range(g):
             bq[i], bs[i] = _quant_b(n, k, gen, dev)
-        def mk(a=a, b=(bq, bs), n=n):
-            a2, b2 = _twin(a), _twin(b)
-            d2 = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
-            return lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a2, b2, d2, idx)
-        nbytes = m_pad * k + g * n * k + 2 * m_pad * n + 4 * m_pad * ((k + 127) // 128) + 4 * m_pad
-        launches.append(Launch(f'n{n}_k{k}', mk, 2 * total * n * k, nbytes))
-    cfg = {'workload': 'm_grouped_fp8_gemm_nt_contiguous 8 experts 32768 tokens Dirichlet(1)',
-           'tokens_per_expert': [int(v) for v in ms], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)]}
-    return launches, cfg, 'mfma'
+        shapes.append(dict(name=f'n{n}_k{k}', n=n, k=k, a=a, b=(bq, bs)))
+    return dict(num_groups=g, total=total, ms=[int(v) for v in ms], aligned=aligned, m_pad=m_pad,
+                m_indices=idx, shapes=shapes)
 
 
-def make_masked():
+def masked_operands(dev='cuda:0'):
+    """Config 4: 16 experts, max_m = 256, masked_m ~ U{96..160}; SFA rows past
+    masked_m are zero (reference tests/generators.py:476-478)."""
     import numpy as np
     import torch
-    import deep_gemm
-    dev = torch.device('cuda:0')
     gen = torch.Generator().manual_seed(0)
     rng = np.random.default_rng(0)
     g, max_m = 16, 256
     masked = rng.integers(96, 161, size=g).astype(np.int32)
-    mm = torch.from_numpy(masked).to(dev)
-    sum_m = int(masked.sum())
-    launches = []
+    shapes = []
     for n, k in [(4096, 7168), (7168, 2048)]:
         aq = torch.empty((g, max_m, k), dtype=torch.float8_e4m3fn, device=dev)
         as_ = torch.empty((g, max_m, (k + 127) // 128), device=dev)
@@ -190,22 +173,17 @@ def make_masked():
             aq[i], as_[i] = _quant_a(max_m, k, gen, dev)
             as_[i, int(masked[i]):] = 0
             bq[i], bs[i] = _quant_b(n, k, gen, dev)
-        def mk(a=(aq, as_), b=(bq, bs), n=n):
-            a2, b2 = _twin(a), _twin(b)
-            d2 = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
-            return lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked(a2, b2, d2, mm, 128)
-        nbytes = g * n * k + sum_m * k + 2 * sum_m * n + 4 * sum_m * ((k + 127) // 128) + \
-            4 * g * ((n + 127) // 128) * ((k + 127) // 128)
-        launches.append(Launch(f'n{n}_k{k}', mk, 2 * sum_m * n * k, nbytes))
-    cfg = {'workload': 'm_grouped_fp8_gemm_nt_masked 16 experts max_m=256 masked_m~U[96,160]',
-           'masked_m': masked.tolist(), 'nk': [(4096, 7168), (7168, 2048)]}
-    return launches, cfg, 'hbm'
+        shapes.append(dict(name=f'n{n}_k{k}', n=n, k=k, a=(aq, as_), b=(bq, bs)))
+    return dict(num_groups=g, max_m=max_m, masked_m=masked, masked_m_dev=torch.from_numpy(masked).to(dev),
+                expected_m=128, shapes=shapes)
 
 
-def make_fp8fp4():
+def fp8fp4_operands(dev='cuda:0'):
+    """Config 5: M = 4096, N = K = 7168; A e4m3 with 1x128 UE8M0 scales, B e2m1
+    with 1x32 UE8M0 scales. Returns the FP32 (power-of-two) scales and their
+    packed MN-major UE8M0 form, which the launches use."""
     import torch
     import deep_gemm
-    dev = torch.device('cuda:0')
     gen = torch.Generator().manual_seed(0)
     m, n, k = 4096, 7168, 7168
     a = deep_gemm.per_token_cast_to_fp8(torch.randn((m, k), generator=gen).bfloat16().to(dev), use_ue8m0=True)
@@ -214,17 +192,100 @@ def make_fp8fp4():
     # Scales in the kernel's packed MN-major UE8M0 form, transformed once up front
     # as for weights (the reference transforms FP32 SFs inside each call and times
     # the GEMM kernel alone, tests/test_fp8_fp4.py:84-86,100).
-    a = (a[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(a[1]))
-    b = (b[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(b[1]))
+    packed_a = (a[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(a[1]))
+    packed_b = (b[0], deep_gemm.get_mn_major_tma_aligned_packed_ue8m0_tensor(b[1]))
+    return dict(m=m, n=n, k=k, a=packed_a, b=packed_b, sfa_f32=a[1], sfb_f32=b[1])
+
+
+def _dense_bytes(m, n, k, out_bytes):
+    return m * k + n * k + 4 * m * ((k + 127) // 128) + 4 * ((n + 127) // 128) * ((k + 127) // 128) + out_bytes
+
+
+def make_dense(acc: bool):
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    launches = []
+    for op in dense_operands(acc, dev):
+        m, n, k = op['m'], op['n'], op['k']
+        if acc:
+            def mk(a=op['a'], b=op['b'], d=op['c']):
+                a2, b2, d2 = _twin(a), _twin(b), _twin(d)
+                return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2, c=d2)
+            out_bytes = 8 * m * n
+        else:
+            def mk(a=op['a'], b=op['b'], m=m, n=n):
+                a2, b2 = _twin(a), _twin(b)
+                d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+                return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2)
+            out_bytes = 2 * m * n
+        launches.append(Launch(op['name'], mk, 2 * m * n * k, _dense_bytes(m, n, k, out_bytes)))
+    cfg = {'workload': 'fp8_gemm_nt M=4096 DeepSeek-V3 (N,K) sweep' + (' FP32 C-accumulate' if acc else ''),
+           'm': 4096, 'nk': DENSE_NK, 'out': 'f32 (D=C+AB^T)' if acc else 'bf16',
+           'recipe': '1x128 A / 128x128 B FP32 scales'}
+    return launches, cfg
+
+
+def make_contiguous():
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    ops = contiguous_operands(dev)
+    g, m_pad, total, idx = ops['num_groups'], ops['m_pad'], ops['total'], ops['m_indices']
+    launches = []
+    for op in ops['shapes']:
+        n, k = op['n'], op['k']
+
+        def mk(a=op['a'], b=op['b'], n=n):
+            a2, b2 = _twin(a), _twin(b)
+            d2 = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
+            return lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a2, b2, d2, idx)
+        nbytes = m_pad * k + g * n * k + 2 * m_pad * n + 4 * m_pad * ((k + 127) // 128) + \
+            4 * g * ((n + 127) // 128) * ((k + 127) // 128) + 4 * m_pad
+        launches.append(Launch(op['name'], mk, 2 * total * n * k, nbytes))
+    cfg = {'workload': 'm_grouped_fp8_gemm_nt_contiguous 8 experts 32768 tokens Dirichlet(1)',
+           'tokens_per_expert': ops['ms'], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)]}
+    return launches, cfg
+
+
+def make_masked():
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    ops = masked_operands(dev)
+    g, max_m, masked, mm = ops['num_groups'], ops['max_m'], ops['masked_m'], ops['masked_m_dev']
+    sum_m = int(masked.sum())
+    launches = []
+    for op in ops['shapes']:
+        n, k = op['n'], op['k']
+
+        def mk(a=op['a'], b=op['b'], n=n):
+            a2, b2 = _twin(a), _twin(b)
+            d2 = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
+            return lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked(a2, b2, d2, mm, ops['expected_m'])
+        nbytes = g * n * k + sum_m * k + 2 * sum_m * n + 4 * sum_m * ((k + 127) // 128) + \
+            4 * g * ((n + 127) // 128) * ((k + 127) // 128)
+        launches.append(Launch(op['name'], mk, 2 * sum_m * n * k, nbytes))
+    cfg = {'workload': 'm_grouped_fp8_gemm_nt_masked 16 experts max_m=256 masked_m~U[96,160]',
+           'masked_m': masked.tolist(), 'nk': [(4096, 7168), (7168, 2048)]}
+    return launches, cfg
+
+
+def make_fp8fp4():
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    op = fp8fp4_operands(dev)
+    m, n, k = op['m'], op['n'], op['k']
 
     def mk():
-        a2, b2 = _twin(a), _twin(b)
+        a2, b2 = _twin(op['a']), _twin(op['b'])
         d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         return lambda: deep_gemm.fp8_fp4_gemm_nt(a2, b2, d2, recipe_a=(1, 128), recipe_b=(1, 32))
     nbytes = m * k + n * k // 2 + 4 * m * (k // 128) + 4 * n * (k // 32) + 2 * m * n
     cfg = {'workload': 'fp8_fp4_gemm_nt M=4096 N=K=7168, A e4m3 1x128 UE8M0, B e2m1 1x32 UE8M0', 'm': m, 'n': n,
            'k': k}
-    return [Launch('m4096_n7168_k7168', mk, 2 * m * n * k, nbytes)], cfg, 'mfma'
+    return [Launch('m4096_n7168_k7168', mk, 2 * m * n * k, nbytes)], cfg
 
 
 def make_kgrouped():
@@ -257,7 +318,7 @@ def make_kgrouped():
     nbytes = sum_k * (m + n) + 4 * (m + n) * (sum_k // 128) + 8 * g * m * n
     cfg = {'workload': 'k_grouped_fp8_gemm_nt_contiguous 8 groups M=4096 N=7168 K_g~4096 (1D1D, FP32 D += )',
            'ks': ks}
-    return [Launch(f'g{g}_m{m}_n{n}_sumk{sum_k}', mk, 2 * m * n * sum_k, nbytes)], cfg, 'mfma'
+    return [Launch(f'g{g}_m{m}_n{n}_sumk{sum_k}', mk, 2 * m * n * sum_k, nbytes)], cfg
 
 
 CAST_MK = [(4096, 7168), (4096, 16384), (4096, 1536), (32768, 7168)]
@@ -277,30 +338,62 @@ def make_cast():
         nbytes = 2 * m * k + m * k + 4 * m * ((k + 127) // 128)
         launches.append(Launch(f'm{m}_k{k}', mk, 0, nbytes))
     cfg = {'workload': 'per_token_cast_to_fp8 bf16 -> e4m3 + MN-major FP32 1x128 SFA', 'mk': CAST_MK}
-    return launches, cfg, 'hbm'
+    return launches, cfg
 
 
 # ---------------------------------------------------------------- CPU baseline
 
+def _cpu_model() -> str:
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or 'unknown'
+
+
+def _median_time(fn, runs: int = 3) -> float:
+    """One untimed warm-up call, then the median of `runs` timed calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def cpu_baseline(workload: str, sample_m: int):
-    """Time the oracle's FP32 dequantize-then-matmul on the host (bounded sample)."""
+    """Time the oracle on the host on a bounded sample of the workload: the FP32
+    dequantize-then-matmul the reference's tests use as their reference path
+    (numpy dequantize, float32 BLAS matmul), or the numpy quantizer for the cast.
+    One warm-up, then the median of 3 timed runs."""
     import numpy as np
     import torch
     from oracle import gemm as ogemm, quant as oquant
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else os.cpu_count()
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, 'sched_getaffinity') else os.cpu_count()
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max((p.get('num_threads', 0) for p in threadpool_info() if p.get('user_api') == 'blas'),
+                           default=0) or None
+    except Exception:   # threadpoolctl absent: report what numpy's BLAS would take by default
+        blas_threads = None
+    host = {'cpu_model': _cpu_model(), 'os_cpu_count': os.cpu_count(), 'affinity_cpus': affinity,
+            'torch_threads': torch.get_num_threads(), 'blas_threads': blas_threads, 'timing': 'median of 3 after 1 warm-up'}
     if workload == 'cast':
         rows = 32 * sample_m   # the cast is far cheaper per row than a GEMM row
         nbytes, secs = 0, 0.0
         for _, k in CAST_MK:
             x = torch.randn((rows, k), generator=torch.Generator().manual_seed(1)).bfloat16().float().numpy()
-            t0 = time.perf_counter()
-            oquant.per_token_cast_to_fp8(x, use_ue8m0=False)
-            secs += time.perf_counter() - t0
+            secs += _median_time(lambda: oquant.per_token_cast_to_fp8(x, use_ue8m0=False))
             nbytes += 3 * rows * k + 4 * rows * ((k + 127) // 128)
-        return {'value': round(nbytes / secs / 1e9, 3), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
-                'sample': f'M={rows} rows of each (M,K) shape: the oracle\'s numpy per-token cast '
-                          f'(single-threaded numpy), {secs:.1f} s total'}
-    rng = np.random.default_rng(0)
+        return dict({'value': round(nbytes / secs / 1e9, 3), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
+                     'sample': f'M={rows} rows of each (M,K) shape: the oracle\'s numpy per-token cast '
+                               f'(single-threaded numpy), {secs:.2f} s per pass (median)'}, **host)
     nk = DENSE_NK if workload in ('dense', 'dense_acc') else [(4096, 7168), (7168, 2048)]
     flops, secs = 0, 0.0
     for n, k in nk:
@@ -308,14 +401,14 @@ def cpu_baseline(workload: str, sample_m: int):
         b = torch.randn((n, k), generator=torch.Generator().manual_seed(2)).bfloat16().float().numpy()
         qa, sfa = oquant.per_token_cast_to_fp8(a, use_ue8m0=False)
         qb, sfb = oquant.per_block_cast_to_fp8(b, use_ue8m0=False)
-        t0 = time.perf_counter()
-        ogemm.gemm_nt_f32(oquant.dequant_per_token(qa, sfa), oquant.dequant_per_block(qb, sfb))
-        secs += time.perf_counter() - t0
+        secs += _median_time(lambda: ogemm.gemm_nt_f32(oquant.dequant_per_token(qa, sfa),
+                                                       oquant.dequant_per_block(qb, sfb)))
         flops += 2 * sample_m * n * k
-    del rng
-    return {'value': round(flops / secs / 1e12, 4), 'unit': 'TFLOPS', 'cores': cores, 'kind': 'port',
-            'sample': f'M={sample_m} rows of each (N,K) shape of the workload: FP32 dequantize (numpy) + '
-                      f'FP32 matmul (numpy BLAS, {cores} host threads), one pass, {secs:.1f} s total'}
+    threads = blas_threads or affinity
+    return dict({'value': round(flops / secs / 1e12, 4), 'unit': 'TFLOPS', 'cores': threads, 'kind': 'port',
+                 'sample': f'M={sample_m} rows of each (N,K) shape of the workload: FP32 dequantize (numpy) + '
+                           f'FP32 matmul (numpy BLAS, {threads} host threads), {secs:.2f} s per pass (median)'},
+                **host)
 
 
 def load_traffic(workload, launches, configs):
@@ -334,6 +427,123 @@ def load_traffic(workload, launches, configs):
     return sum(per[l.name]['total'] for l in launches), f'profiles/{os.path.basename(path)}'
 
 
+# ---------------------------------------------------------------- timing
+
+MAKERS = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
+          'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast,
+          'kgrouped': make_kgrouped}
+# Configurations summarized next to the headline in the default run (per-launch
+# kernel time and roofline fraction; the headline `value` stays config 2).
+EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4']
+
+
+def t_min_us(flops, nbytes):
+    """Roofline time of one launch: max(FLOPs / FP8 peak, bytes / HBM peak), in us."""
+    return max(flops / (PEAK_FP8_TFLOPS * 1e6), nbytes / (PEAK_HBM_GBS * 1e3))
+
+
+class Workload:
+    """A workload's launches, each with `rot` rotating buffer sets, plus (unless
+    eager) one HIP graph per launch over its sets and one per set over all
+    launches."""
+
+    def __init__(self, name, rot, eager):
+        import torch
+        import deep_gemm
+        self.name, self.rot, self.eager = name, rot, eager
+        self.launches, self.cfg = MAKERS[name]()
+        # Rotating buffer sets: fns[i][r] runs launch i on its own copy r of the
+        # inputs and outputs, so consecutive launches never find their operands in
+        # L2 or the Infinity Cache (the sets of a step span well over 288 MB).
+        self.fns = [[l.mk() for _ in range(rot)] for l in self.launches]
+        torch.cuda.synchronize()
+        # One eager pass over every set: library initialisation, and the kernel
+        # configuration each launch resolves to.
+        self.configs = []
+        for i in range(len(self.launches)):
+            for r in range(rot):
+                self.fns[i][r]()
+            self.configs.append(deep_gemm.get_last_config())
+        torch.cuda.synchronize()
+        # HIP graphs (the library records into a capturing stream like any other);
+        # replays take the Python launch overhead out of the timed regions.
+        self.launch_graphs, self.step_graphs = [], []
+        if not eager:
+            for i in range(len(self.launches)):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for r in range(rot):
+                        self.fns[i][r]()
+                self.launch_graphs.append(g)
+            for r in range(rot):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for i in range(len(self.launches)):
+                        self.fns[i][r]()
+                self.step_graphs.append(g)
+            torch.cuda.synchronize()
+
+    def run_launch(self, i):
+        if self.eager:
+            for r in range(self.rot):
+                self.fns[i][r]()
+        else:
+            self.launch_graphs[i].replay()
+
+    def run_step(self, sidx):
+        if self.eager:
+            for i in range(len(self.launches)):
+                self.fns[i][sidx % self.rot]()
+        else:
+            self.step_graphs[sidx % self.rot].replay()
+
+    def per_launch_us(self, reps):
+        """Per-launch kernel durations: HIP events on the launch stream (torch's
+        current stream, which the library and the graph replays launch on) around
+        the launch run over all of its sets, / rot, with L2 and the 256 MB Infinity
+        Cache flushed before each run, as the reference's bench_kineto flushes L2
+        (deep_gemm/testing/bench.py:76-104), so operands come from HBM. The flush
+        READS a 512 MiB buffer instead of zero-filling one: a fill leaves up to
+        288 MB of dirty lines in L2 and the memory-side Infinity Cache whose
+        write-back then lands inside the next timed kernel (up to 30% of an
+        HBM-bound launch here); a read evicts the operands without that backlog."""
+        import torch
+        stream = torch.cuda.current_stream()
+        flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device='cuda:0')
+        per = []
+        for i, l in enumerate(self.launches):
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for e0, e1 in evs:
+                torch.sum(flush, dtype=torch.int64)
+                e0.record(stream)
+                self.run_launch(i)
+                e1.record(stream)
+            torch.cuda.synchronize()
+            us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / (reps * self.rot)
+            per.append(us)
+            log(f'  [{self.name}] {l.name}: {us:8.1f} us  {l.flops / us / 1e6:7.1f} TFLOPS  '
+                f'{l.nbytes / us / 1e3:7.1f} GB/s  roofline {t_min_us(l.flops, l.nbytes) / us:.3f}  [{self.configs[i]}]')
+        del flush
+        return per
+
+    def summary(self, per):
+        """Per-launch and aggregate roofline scoring: each launch against its own
+        bound t_min = max(FLOPs / P_fp8, bytes / BW); the aggregate fraction is
+        sum(t_min) / sum(t_measured)."""
+        t_mins = [t_min_us(l.flops, l.nbytes) for l in self.launches]
+        bounds = ['mfma' if l.flops / (PEAK_FP8_TFLOPS * 1e6) >= l.nbytes / (PEAK_HBM_GBS * 1e3) else 'hbm'
+                  for l in self.launches]
+        return {
+            'workload': self.cfg['workload'],
+            'frac': round(sum(t_mins) / sum(per), 4),
+            'kernel_us': round(sum(per), 2),
+            'per_launch': {l.name: {'us': round(u, 2), 'tflops': round(l.flops / u / 1e6, 1),
+                                    'gbs': round(l.nbytes / u / 1e3, 1), 'bound': b,
+                                    'frac': round(tm / u, 4), 'config': c}
+                           for l, u, tm, b, c in zip(self.launches, per, t_mins, bounds, self.configs)},
+        }
+
+
 # ---------------------------------------------------------------- main
 
 def main():
@@ -343,11 +553,7 @@ def main():
               f'(requested --gpus {args.gpus}); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     import torch
-    import deep_gemm
     torch.cuda.set_device(0)
-    makers = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
-              'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast,
-              'kgrouped': make_kgrouped}
     if args.calibrate_copy_mib > 0:
         x = torch.randn(args.calibrate_copy_mib * 1024 * 256, device='cuda:0')
         y = torch.empty_like(x)
@@ -355,124 +561,63 @@ def main():
             torch.neg(x, out=y)
         torch.cuda.synchronize()
         del x, y
-    launches, cfg, bound = makers[args.workload]()
     rot = args.rotate
-    # Rotating buffer sets: fns[i][r] runs launch i on its own copy r of the
-    # inputs and outputs, so consecutive launches never find their operands in
-    # L2 or the Infinity Cache (the sets of a step span well over 288 MB).
-    fns = [[l.mk() for _ in range(rot)] for l in launches]
-    torch.cuda.synchronize()
-    log(f'workload {args.workload}: {len(launches)} launches per step, {rot} rotating buffer sets')
-
-    # One eager pass over every set: library initialisation, and the kernel
-    # configuration each launch resolves to.
-    configs = []
-    for i in range(len(launches)):
-        for r in range(rot):
-            fns[i][r]()
-        configs.append(deep_gemm.get_last_config())
-    torch.cuda.synchronize()
-
-    # HIP graphs (the library records into a capturing stream like any other):
-    # one per launch over its sets (per-launch timing) and one per set over all
-    # launches (one step). Replays take the Python launch overhead out of both
-    # timed regions; --eager launches from Python instead.
-    if not args.eager:
-        launch_graphs, step_graphs = [], []
-        for i in range(len(launches)):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                for r in range(rot):
-                    fns[i][r]()
-            launch_graphs.append(g)
-        for r in range(rot):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                for i in range(len(launches)):
-                    fns[i][r]()
-            step_graphs.append(g)
-        torch.cuda.synchronize()
-
-    def run_launch(i):
-        if args.eager:
-            for r in range(rot):
-                fns[i][r]()
-        else:
-            launch_graphs[i].replay()
-
-    def run_step(sidx):
-        if args.eager:
-            for i in range(len(launches)):
-                fns[i][sidx % rot]()
-        else:
-            step_graphs[sidx % rot].replay()
-
-    # Per-launch durations: HIP events on the launch stream (torch's current
-    # stream, which the library and graph replays launch on) around the launch
-    # run over all of its sets, with L2 and the 256 MB Infinity Cache flushed
-    # before it, as the reference's bench_kineto flushes L2
-    # (deep_gemm/testing/bench.py:76-104), so operands come from HBM. The flush
-    # READS a 512 MiB buffer instead of zero-filling one: a fill leaves up to
-    # 288 MB of dirty lines in L2 and the memory-side Infinity Cache whose
-    # write-back then lands inside the next timed kernel (up to 30% of an
-    # HBM-bound launch here); a read evicts the operands without that backlog.
-    stream = torch.cuda.current_stream()
-    flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device='cuda:0')
     reps = max(5, args.steps)
-    per = []
-    for i, l in enumerate(launches):
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for e0, e1 in evs:
-            torch.sum(flush, dtype=torch.int64)
-            e0.record(stream)
-            run_launch(i)
-            e1.record(stream)
-        torch.cuda.synchronize()
-        us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / (reps * rot)
-        per.append(us)
-        log(f'  {l.name}: {us:8.1f} us  {l.flops / us / 1e6:7.1f} TFLOPS  {l.nbytes / us / 1e3:7.1f} GB/s  '
-            f'[{configs[i]}]')
-    del flush
+    wl = Workload(args.workload, rot, args.eager)
+    launches = wl.launches
+    log(f'workload {args.workload}: {len(launches)} launches per step, {rot} rotating buffer sets')
+    per = wl.per_launch_us(reps)
 
     for w in range(args.warmup):
-        run_step(w)
+        wl.run_step(w)
     # Whole-job timed region: K steps, synchronized on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for sidx in range(args.steps):
-        run_step(sidx)
+        wl.run_step(sidx)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     total_flops = sum(l.flops for l in launches) * args.steps
     total_bytes = sum(l.nbytes for l in launches)
     value = total_flops / elapsed / 1e12
-    if total_flops == 0:   # a byte-moving workload (cast): GB/s
+    cast = args.workload == 'cast'
+    if cast:   # a byte-moving workload: GB/s
         value = total_bytes * args.steps / elapsed / 1e9
 
+    summ = wl.summary(per)
     kernel_us = sum(per)
-    if bound == 'mfma':
-        peak = PEAK_FP8_TFLOPS
-        achieved = sum(l.flops for l in launches) / kernel_us / 1e6
-        unit = 'TFLOP/s'
+    t_mins = [t_min_us(l.flops, l.nbytes) for l in launches]
+    mfma_t = sum(l.flops / (PEAK_FP8_TFLOPS * 1e6) for l in launches)
+    hbm_t = sum(l.nbytes / (PEAK_HBM_GBS * 1e3) for l in launches)
+    bound = 'mfma' if mfma_t >= hbm_t else 'hbm'
+    if all(b['bound'] == bound for b in summ['per_launch'].values()):
+        # every launch has the same bound: the plain rate against that peak
+        achieved = (sum(l.flops for l in launches) / kernel_us / 1e6 if bound == 'mfma'
+                    else total_bytes / kernel_us / 1e3)
+        how = (f'algorithmic {"FLOPs" if bound == "mfma" else "bytes"} of the step / sum of per-launch durations')
     else:
-        peak = PEAK_HBM_GBS
-        achieved = total_bytes / kernel_us / 1e3
-        unit = 'GB/s'
-    traffic, traffic_note = load_traffic(args.workload, launches, configs)
-    roofline = {'bound': bound, 'achieved': round(achieved, 2), 'peak': peak, 'unit': unit,
+        # mixed bounds: each launch is scored against its own roofline time, and the
+        # step's rate is that fraction of the dominant bound's peak
+        achieved = sum(t_mins) / kernel_us * (PEAK_FP8_TFLOPS if bound == 'mfma' else PEAK_HBM_GBS)
+        how = ('peak-equivalent rate: sum over launches of t_min = max(FLOPs/P_fp8, bytes/BW), / sum of '
+               'per-launch durations, x the dominant bound\'s peak')
+    peak = PEAK_FP8_TFLOPS if bound == 'mfma' else PEAK_HBM_GBS
+    traffic, traffic_note = load_traffic(args.workload, launches, wl.configs)
+    roofline = {'bound': bound, 'achieved': round(achieved, 2), 'peak': peak,
+                'unit': 'TFLOP/s' if bound == 'mfma' else 'GB/s',
                 'frac': round(achieved / peak, 4), 'traffic': traffic,
-                'per': f'one step = {len(launches)} launch(es), one per shape; achieved = algorithmic '
-                       f'{"FLOPs" if bound == "mfma" else "bytes"} of the step / sum of per-launch durations '
-                       f'(each the event time of {rot} back-to-back launches on rotating buffer sets after a '
-                       f'cache flush, / {rot}); traffic = calibrated HBM bytes (FETCH_SIZE + WRITE_SIZE) of the step',
+                'per': f'one step = {len(launches)} launch(es), one per shape; achieved = {how} (each the event '
+                       f'time of {rot} back-to-back launches on rotating buffer sets after a cache flush, / {rot}); '
+                       f'traffic = calibrated HBM bytes (FETCH_SIZE + WRITE_SIZE) of the step',
                 'traffic_source': traffic_note,
-                'kernel': sorted({c.split(' kind=')[0] for c in configs}),
-                'launch_config': {l.name: c for l, c in zip(launches, configs)},
+                'kernel': sorted({c.split(' kind=')[0] for c in wl.configs}),
+                'launch_config': {l.name: c for l, c in zip(launches, wl.configs)},
                 'algorithmic_bytes': {l.name: l.nbytes for l in launches},
                 'per_launch_us': {l.name: round(u, 2) for l, u in zip(launches, per)},
                 'per_launch_tflops': {l.name: round(l.flops / u / 1e6, 1) for l, u in zip(launches, per)},
-                'per_launch_gbs': {l.name: round(l.nbytes / u / 1e3, 1) for l, u in zip(launches, per)}}
-    cast = args.workload == 'cast'
+                'per_launch_gbs': {l.name: round(l.nbytes / u / 1e3, 1) for l, u in zip(launches, per)},
+                'per_launch_frac': {k: v['frac'] for k, v in summ['per_launch'].items()},
+                'per_launch_bound': {k: v['bound'] for k, v in summ['per_launch'].items()}}
     out = {
         'metric': ('FP8 per-token activation cast GB/s (bf16 -> e4m3 + 1x128 SFA)' if cast else
                    'FP8 block-scaled GEMM TFLOPS + % of MI355X FP8 MFMA peak, DSV3 shapes'),
@@ -488,11 +633,24 @@ def main():
         'dtype': ('bf16 -> e4m3' if cast else
                   'e4m3 (fp32 accumulate)' if args.workload != 'fp8fp4' else 'e4m3 x e2m1 (fp32 accumulate)'),
         'data': 'synthetic (seeded randn, bf16 -> quantized)',
-        'config': cfg,
+        'config': wl.cfg,
         'timing': {'launch': 'eager (Python)' if args.eager else 'hipGraph replay', 'rotating_sets': rot,
                    'per_launch_reps': reps},
         'roofline': roofline,
     }
+    del wl
+    torch.cuda.empty_cache()
+    # The other configurations, kernel time and roofline fraction per launch
+    # (not part of `value`, which is the headline configuration's whole-job rate).
+    if args.workload == 'dense' and not args.no_extras:
+        extras = {}
+        for name in EXTRAS:
+            log(f'extra workload {name} ...')
+            w = Workload(name, rot, args.eager)
+            extras[name] = w.summary(w.per_launch_us(reps))
+            del w
+            torch.cuda.empty_cache()
+        out['other_configs'] = extras
     if not args.no_cpu_baseline:
         log('cpu baseline ...')
         out['cpu_baseline'] = cpu_baseline(args.workload, args.cpu_sample_m)

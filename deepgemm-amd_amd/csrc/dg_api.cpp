@@ -291,6 +291,10 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     for (const auto& c : cands) {
         if (!grouped_tile_ok(kind, c.variant, c.bm, align_m)) continue;
         if (c.variant == 2 && !pipe_ok) continue;
+        // K % 128 != 0: the 256 x 256 pipelined tile's K-tail schedule (per-lane
+        // 64-bit load addresses next to 256 registers of accumulators) spills to
+        // scratch; the other tiles' K-tail schedules do not.
+        if (c.variant == 2 && c.bm == 256 && c.bn == 256 && k % 128 != 0) continue;
         const int64_t tiles = ceil_div(m_rows, c.bm) * ceil_div(n, c.bn) * groups;
         const int64_t slots = (int64_t)cus * c.per_cu;
         const double rounds = (double)ceil_div(tiles, slots);

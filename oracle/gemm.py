@@ -17,6 +17,14 @@ Functions and what they follow:
                            -- expert of an M-block is ``max(0, layout[block*BM])``
                               (``scheduler/gemm.cuh:150-153``); rows with layout
                               < 0 are padding (``:299-300``) and stay untouched.
+* ``psum_blocks`` / ``gemm_psum``
+                           -- the psum-layout walk (``scheduler/gemm.cuh:92-94``
+                              init, ``:205-225`` get_next_block, ``:306-307``
+                              validity): group i owns the M blocks from
+                              align(psum[i-1], BLOCK_M) up to psum[i]; rows
+                              [psum[i], align(psum[i], alignment)) are padding,
+                              zero-filled with ``ensure_zero_padding``
+                              (``tests/utils.py:9-18``) and untouched otherwise.
 * ``gemm_masked``          -- rows r < masked_m[g] of group g are computed
                               (``scheduler/gemm.cuh:188-204,301-302``); the rest
                               stay untouched.
@@ -95,6 +103,58 @@ def gemm_contiguous(a_deq: np.ndarray, b_deq: np.ndarray, m_indices: np.ndarray,
         if rows.size:
             d[rows] = a_deq[rows].astype(np.float64) @ b_deq[e].astype(np.float64).T
     return d, valid
+
+
+def _align(x: int, y: int) -> int:
+    return (x + y - 1) // y * y
+
+
+def psum_blocks(psum, block_m: int):
+    """The psum walk of ``scheduler/gemm.cuh:205-225`` over M blocks (the N blocks
+    of a row of tiles repeat it): returns [(group, m_block_idx, row_end)] in walk
+    order, where the block computes rows [m_block_idx * block_m, row_end) clipped
+    to the block.
+
+    Walk state as in the reference: group 0 starts at row 0 with
+    ceil(psum[0] / block_m) blocks (``:92-94``); moving to group i sets
+    last = align(psum[i-1], block_m) and gives it ceil((psum[i] - last) / block_m)
+    blocks numbered from last / block_m (``:215-224``). The reference keeps these
+    counts in uint32, which assumes psum[i] >= align(psum[i-1], block_m) (the
+    layout its generator builds, ``tests/generators.py:459``); that is asserted."""
+    psum = [int(v) for v in psum]
+    out = []
+    last, cur = 0, psum[0]
+    for g in range(len(psum)):
+        if g:
+            last, cur = _align(cur, block_m), psum[g]
+            assert cur >= last, 'psum layout: each group must start at or after the aligned end of the previous one'
+        nmb = (cur - last + block_m - 1) // block_m
+        for j in range(nmb):
+            out.append((g, last // block_m + j, cur))
+    return out
+
+
+def gemm_psum(a_deq: np.ndarray, b_deq: np.ndarray, psum, block_m: int, alignment: int, zero_padding: bool):
+    """Contiguous GEMM in the psum layout -> (D float64 [M, N], NaN where the
+    call must leave D untouched; written mask [M]). Computed rows follow
+    ``psum_blocks``; rows [psum[i], align(psum[i], alignment)) are 0 with
+    ``zero_padding`` (``tests/utils.py:9-18``), untouched without."""
+    m = a_deq.shape[0]
+    n = b_deq.shape[1]
+    d = np.full((m, n), np.nan, dtype=np.float64)
+    written = np.zeros(m, dtype=bool)
+    for g, mb, row_end in psum_blocks(psum, block_m):
+        r0, r1 = mb * block_m, min((mb + 1) * block_m, row_end, m)
+        if r1 > r0:
+            d[r0:r1] = a_deq[r0:r1].astype(np.float64) @ b_deq[g].astype(np.float64).T
+            written[r0:r1] = True
+    if zero_padding:
+        for end in psum:
+            p0, p1 = int(end), min(_align(int(end), alignment), m)
+            if p1 > p0:
+                d[p0:p1] = 0.0
+                written[p0:p1] = True
+    return d, written
 
 
 def gemm_masked(a_deq: np.ndarray, b_deq: np.ndarray, masked_m: np.ndarray):

@@ -11,12 +11,17 @@ step is done in float32 with IEEE rounding, in the reference's order:
     sf   = ceil_to_ue8m0(sf)    when use_ue8m0
     q    = cast(x * (1 / sf))   (float32 reciprocal, float32 product, RNE cast)
 
-The reference writes ``sf = amax / 448.0`` and runs it on the GPU, where torch's
-division of a tensor by a Python scalar multiplies by the scalar's float32
-reciprocal (PyTorch's CUDA/ROCm true-divide kernel); that product, not the
-correctly rounded quotient, is what DeepGEMM's tests feed the GEMM (they differ
-by one ulp in a few percent of groups). The oracle restates the GPU behaviour;
-``tests/test_gemm_gpu.py::test_product_quantizers_match_oracle_on_gpu`` pins it.
+The reference writes ``sf = amax / 448.0`` (``/ 6.0`` for FP4) and runs it on
+the GPU. PyTorch's true-divide kernel for CUDA/ROCm, when the divisor is a
+Python scalar, multiplies by the scalar's float32 reciprocal instead of
+dividing, so the reference's scales are ``amax * fl32(1/448)``. That product
+and the correctly rounded quotient differ by one ulp for about half of all
+float32 amax values (torch on the CPU does divide, and gives the other one).
+``scale_from_amax`` restates the GPU behaviour.
+``tests/test_quant_pin_gpu.py`` pins it against torch's own ``amax / 448.0`` and
+``/ 6.0`` on the GPU over 3.8e5 amax values, 1e5 of them values where the
+two roundings differ, and pins the reciprocal and cast steps with the
+reference's whole torch sequence on the GPU.
 
 Functions and the reference lines they follow:
 
@@ -36,12 +41,19 @@ import numpy as np
 from . import fp8
 
 
-_INV_E4M3_MAX = np.float32(1.0 / 448.0)   # fl32 of the reciprocal, as torch applies it
-_INV_E2M1_MAX = np.float32(1.0 / 6.0)
+E4M3_MAX = 448.0
+E2M1_MAX = 6.0
 
 
 def _align(x: int, y: int) -> int:
     return (x + y - 1) // y * y
+
+
+def scale_from_amax(amax: np.ndarray, max_code: float) -> np.ndarray:
+    """sf = amax / max_code as torch computes it on the GPU (``deep_gemm/utils/math.py:36,69,111``):
+    amax times the float32 reciprocal of the Python scalar, one float32 rounding."""
+    inv = np.float32(1.0) / np.float32(max_code)
+    return (np.asarray(amax, dtype=np.float32) * inv).astype(np.float32)
 
 
 def _recip_f32(sf: np.ndarray) -> np.ndarray:
@@ -58,7 +70,7 @@ def per_token_cast_to_fp8(x: np.ndarray, use_ue8m0: bool, gran_k: int = 128):
     xp[:, :n] = x
     xv = xp.reshape(m, pn // gran_k, gran_k)
     amax = np.maximum(np.abs(xv).max(axis=2), np.float32(1e-4)).astype(np.float32)
-    sf = (amax * _INV_E4M3_MAX).astype(np.float32)
+    sf = scale_from_amax(amax, E4M3_MAX)
     if use_ue8m0:
         sf = fp8.ceil_to_ue8m0(sf)
     scaled = (xv * _recip_f32(sf)[:, :, None]).astype(np.float32)
@@ -76,7 +88,7 @@ def per_block_cast_to_fp8(x: np.ndarray, use_ue8m0: bool, gran_k: int = 128):
     xp[:m, :n] = x
     xv = xp.reshape(pm // gran_k, gran_k, pn // gran_k, gran_k)
     amax = np.maximum(np.abs(xv).max(axis=(1, 3)), np.float32(1e-4)).astype(np.float32)
-    sf = (amax * _INV_E4M3_MAX).astype(np.float32)
+    sf = scale_from_amax(amax, E4M3_MAX)
     if use_ue8m0:
         sf = fp8.ceil_to_ue8m0(sf)
     scaled = (xv * _recip_f32(sf)[:, None, :, None]).astype(np.float32)
@@ -94,7 +106,7 @@ def per_token_cast_to_fp4(x: np.ndarray, use_ue8m0: bool, gran_k: int = 128):
     xp[:, :n] = x
     xv = xp.reshape(m, pn // gran_k, gran_k)
     amax = np.maximum(np.abs(xv).max(axis=2), np.float32(1e-4)).astype(np.float32)
-    sf = (amax * _INV_E2M1_MAX).astype(np.float32)
+    sf = scale_from_amax(amax, E2M1_MAX)
     if use_ue8m0:
         sf = fp8.ceil_to_ue8m0(sf)
     scaled = (xv * _recip_f32(sf)[:, :, None]).astype(np.float32)

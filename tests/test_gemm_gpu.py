@@ -252,6 +252,11 @@ def _contiguous_case(ms, aligned, n, k):
 
 
 def test_psum_layout():
+    """psum layout against the oracle's restatement of the reference's psum walk
+    (oracle/gemm.py psum_blocks / gemm_psum): computed rows match the FP64
+    oracle, rows the call must not write keep the sentinel, the padding rows are
+    zero with ensure_zero_padding (the reference's assert_psum_zero_padding,
+    tests/utils.py:9-18, on both A and D), and each group equals a dense call."""
     g, n, k = 4, 256, 512
     ms = [100, 0, 257, 64]
     align = deep_gemm.get_mk_alignment_for_contiguous_layout()
@@ -265,12 +270,23 @@ def test_psum_layout():
     x = gen.contiguous_inputs(ms, [((mi + align - 1) // align) * align for mi in ms], n, k, seed=21)
     # x rows are laid out with per-group aligned starts, identical to the psum starts above
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    a_deq = oquant.dequant_per_token(x['qa'], x['sfa'])
+    b_deq = np.stack([oquant.dequant_per_block(x['qb'][i], x['sfb'][i]) for i in range(g)])
     psum = torch.tensor(ends, dtype=torch.int32, device=DEV)
     for zero_pad in (False, True):
+        ref, written = ogemm.gemm_psum(a_deq, b_deq, ends, align, align, zero_pad)
         d = sentinel_bf16((m_pad, n))
         deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, psum, use_psum_layout=True,
                                                    ensure_zero_padding=zero_pad)
         torch.cuda.synchronize()
+        out = d.float().cpu().numpy()
+        computed = written & ~np.isnan(ref).any(axis=1) & np.any(ref != 0.0, axis=1)
+        diff, _ = report(f'psum zero_pad={zero_pad}', out[computed], ref[computed])
+        assert diff < 1e-3
+        tol = np.abs(ref[computed]) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref[computed]).max()
+        assert np.all(np.abs(out[computed] - ref[computed]) <= tol)
+        assert np.all(out[written & ~computed] == 0.0)
+        assert bool((d.view(torch.int16)[torch.from_numpy(~written).to(DEV)] == SENTINEL).all()), 'rows touched'
         for i in range(g):
             s, e = starts[i], ends[i]
             if e > s:
@@ -278,11 +294,10 @@ def test_psum_layout():
                 deep_gemm.fp8_gemm_nt((a[0][s:e], a[1][s:e]), (b[0][i], b[1][i]), dd)
                 assert torch.equal(dd.view(torch.int16), d[s:e].view(torch.int16)), f'group {i}'
             pe = (e + align - 1) // align * align
-            pad = d[e:pe].view(torch.int16)
-            if zero_pad:
-                assert bool((pad == 0).all()), f'group {i} padding not zeroed'
-            else:
-                assert bool((pad == SENTINEL).all()), f'group {i} padding touched'
+            if zero_pad and pe > e:
+                # the reference's assert_psum_zero_padding: A and D padding rows are zero
+                assert np.all(x['qa'][e:pe] == 0), f'group {i} A padding not zero'
+                assert bool((d[e:pe].view(torch.int16) == 0).all()), f'group {i} padding not zeroed'
 
 
 @pytest.mark.parametrize('n,k', [(512, 1024), (256, 2048)])

@@ -297,6 +297,52 @@ def test_masked_rules_brute_force():
                 assert np.all(np.isnan(d[g, r]))
 
 
+@pytest.mark.parametrize('seed', range(6))
+def test_psum_rules_brute_force(seed):
+    """psum_blocks / gemm_psum against the layout's own definition, row by row: the
+    reference's generator puts group i's rows at [align(psum[i-1]), psum[i]) with
+    psum[i] = align(psum[i-1]) + m_i (tests/generators.py:422-431,459), and its
+    zero-padding check wants rows [psum[i], align(psum[i])) zero (tests/utils.py:9-18)."""
+    rng = np.random.default_rng(40 + seed)
+    align = 4
+    counts = rng.integers(0, 11, size=int(rng.integers(1, 6)))
+    counts[rng.integers(0, len(counts))] = 0           # an empty group somewhere
+    psum, prev = [], 0
+    for c in counts:
+        prev = (prev + align - 1) // align * align + int(c)
+        psum.append(prev)
+    m = (psum[-1] + align - 1) // align * align + align   # a spare block past the last group
+    owner = np.full(m, -1)
+    start = 0
+    for i, end in enumerate(psum):
+        owner[start:end] = i
+        start = (end + align - 1) // align * align
+    # walk coverage: each owned row once, with its group; no other row
+    seen = np.full(m, -1)
+    for g, mb, row_end in ogemm.psum_blocks(psum, align):
+        for r in range(mb * align, min((mb + 1) * align, row_end)):
+            assert seen[r] == -1, 'row computed twice'
+            seen[r] = g
+    assert np.array_equal(seen, owner), (psum, seen, owner)
+    a = rng.standard_normal((m, 8)).astype(np.float32)
+    b = rng.standard_normal((len(psum), 3, 8)).astype(np.float32)
+    for zero_pad in (False, True):
+        d, written = ogemm.gemm_psum(a, b, psum, align, align, zero_pad)
+        for r in range(m):
+            pad = any(e <= r < (e + align - 1) // align * align for e in psum) and owner[r] < 0
+            if owner[r] >= 0:
+                assert written[r] and np.allclose(d[r], a[r].astype(np.float64) @ b[owner[r]].astype(np.float64).T)
+            elif pad and zero_pad:
+                assert written[r] and np.all(d[r] == 0.0)
+            else:
+                assert not written[r] and np.all(np.isnan(d[r]))
+
+
+def test_psum_rejects_overlapping_groups():
+    with pytest.raises(AssertionError):
+        ogemm.psum_blocks([5, 6], 4)    # group 1 would start at align(5) = 8 > 6
+
+
 def test_calc_diff_closed_forms():
     x = np.random.default_rng(12).standard_normal(1000)
     assert ogemm.calc_diff(x, x) == pytest.approx(0.0, abs=1e-15)
