@@ -26,6 +26,8 @@ thread_local std::string t_last_config;
 // Process-wide knobs (the reference keeps them in lazily created singletons,
 // csrc/runtime/runtime.hpp:104, csrc/jit_kernels/heuristics/runtime.hpp:67).
 constexpr int kDefaultMKAlignment = 128;
+// Dense calls of at most this many rows run on the weight-streaming kernel.
+constexpr int kDenseStreamRows = 16;
 std::atomic<int> g_num_sms{0};                 // 0: query the device
 std::atomic<int> g_mk_alignment{kDefaultMKAlignment};
 std::atomic<int> g_tile_variant{0}, g_tile_m{0}, g_tile_n{0};   // variant 0: heuristic
@@ -414,14 +416,20 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         const int64_t m_rows = m;
         const int tv = g_tile_variant.load();
         TileConfig t;
-        if (tv == 5) {   // forced: the masked weight-streaming kernel
-            if (kind != kMasked || !fp8_masked_stream_supported(args))
-                DG_UNSUPPORTED("tile override: the weight-streaming kernel runs the masked layout with K % 128 == 0");
-            t = {kMaskedStreamRows, g_tile_n.load(), 5};
-        } else if (tv == 0 && kind == kMasked && expected_m <= kMaskedStreamRows && fp8_masked_stream_supported(args)) {
+        // Dense calls of at most kDenseStreamRows rows are weight-stream bound: they
+        // run on the streaming kernel as one group (layout null), which loads only
+        // the rows that exist (16 x 16 x 128 MFMAs up to 16 rows).
+        const bool stream_ok = fp8_masked_stream_supported(args) &&
+                               (kind == kMasked || (kind == kNormal && m_rows <= kDenseStreamRows));
+        if (tv == 5) {   // forced: the weight-streaming kernel
+            if (!stream_ok)
+                DG_UNSUPPORTED("tile override: the weight-streaming kernel runs the masked layout, or dense calls of at "
+                               "most 160 rows, with K % 128 == 0, BF16 D and no C");
+            t = {g_tile_m.load(), g_tile_n.load(), 5};
+        } else if (tv == 0 && stream_ok && (kind == kNormal || expected_m <= kMaskedStreamRows)) {
             // decode-sized groups: the weight-streaming kernel (one pass per group
             // when masked_m <= 160; larger groups take more passes)
-            t = {kMaskedStreamRows, 32 * fp8_masked_stream_waves(n, groups, args.grid_limit), 5};
+            t = {kStream16Rows, 32 * fp8_masked_stream_waves(n, groups, args.grid_limit), 5};
         } else {
             t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
         }
@@ -429,7 +437,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
         if (t.variant == 5)
-            launch_fp8_gemm_masked_stream(args, t.block_n / 32, stream);
+            launch_fp8_gemm_masked_stream(args, t.block_n / 32, t.block_m == kStream16Rows, stream);
         else if (t.variant >= 2)
             launch_fp8_gemm_1d2d_v2(kind, t, args, stream);
         else
@@ -953,7 +961,8 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
         }
         const bool ok = variant == 1   ? fp8_1d2d_tile_supported(block_m, block_n)
                         : variant == 2 ? fp8_1d2d_v2_tile_supported(block_m, block_n)
-                        : variant == 5 ? (block_m == kMaskedStreamRows && block_n % 32 == 0 && block_n >= 128 &&
+                        : variant == 5 ? ((block_m == kMaskedStreamRows || block_m == kStream16Rows) &&
+                                          block_n % 32 == 0 && block_n >= 128 &&
                                           block_n <= 256)
                         : variant == 6 ? (block_m == 128 && (block_n == 128 || block_n == 192 || block_n == 256))
                         : variant == 7 ? (block_m == 256 && block_n == 128)

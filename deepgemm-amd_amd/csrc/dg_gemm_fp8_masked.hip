@@ -25,6 +25,13 @@
 //    per-wave count, so one s_waitcnt vmcnt immediate serves every wave;
 //  * workgroups of one expert run on one XCD (logical tiles are expert-major
 //    and mapped to XCDs in contiguous ranges), so A rows reach HBM once per XCD.
+// A pass of at most 16 rows (small decode groups, and dense calls of at most 16
+// rows, which run here as one group) may instead use v_mfma_f32_16x16x128_f8f6f4:
+// one instruction per 16 x 16 output block and 128-wide K block, so the pass
+// loads and multiplies 16 rows of A instead of a 32-row tile. It keeps the
+// per-K-block promotion; its sums round differently from the 32 x 32 x 64 pair
+// (one 128-product MFMA instead of two 64-product ones), so it is a separate
+// kernel configuration (block_m 16) rather than a bitwise twin.
 // Requirements (checked by the host): K a multiple of 128 with at most 128 K
 // blocks, BF16 D without C, 16-byte aligned A/B/D rows.
 #include <hip/hip_runtime.h>
@@ -244,9 +251,131 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
                                                   (int64_t)g * p.d_gs);
 }
 
+// One pass over rows [r0, r0 + 16) of the group (a_rows <= 16 of them valid)
+// with 16 x 16 x 128 MFMAs: wave w's 32 columns are two 16-column halves h,
+// each one MFMA per K block with the pass's 16 rows. Operand lane l holds row
+// l & 15 and K bytes [32 (l >> 4), +32) of the block (the same bytes for both
+// operands, so every product of the block is summed once); the result lane l
+// holds rows 4 (l >> 4) + e of the half's columns for token l & 15.
+template <int NW>
+__device__ __forceinline__ void masked_pass16(const Fp8GemmArgs& p, uint8_t* smem, const uint8_t* b_t,
+                                              const uint32_t (&voff_b)[StreamShape<NW>::LB], bool b_primed, int g,
+                                              int n0, int r0, int a_rows, int m_g, int wave, int lane) {
+    using S = StreamShape<NW>;
+    constexpr int ROWS = 16;
+    constexpr int A_SEGS = ROWS / 8;   // two 1 KB loads of A, then one 256 B SFA load (16 lanes used)
+    constexpr int A_LOADS = A_SEGS + 1;
+    constexpr int A_STAGE = ROWS * kBK + 256;
+    constexpr int SA = 4;              // small stages: four in flight
+    static_assert(S::B_RING + SA * A_STAGE <= kLds, "LDS");
+    constexpr int LB = S::LB;
+    // Waves 0 .. A_LOADS - 1 issue one A-side load each; the others repeat the
+    // last one (same bytes), so every wave issues exactly one per stage.
+    constexpr int W = 1 + LB;          // loads after A(kb + 1) / B(kb + 1): block kb's own
+    static_assert(1 + LB < 64, "vmcnt range");
+
+    const int num_kb = p.k / kBK;
+    const int rs = lane >> 3, pc = lane & 7;
+    const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
+    const uint32_t a_ring = smem_lds + S::B_RING;
+    const uint8_t* __restrict__ a_p = p.a + (int64_t)g * p.a_gs + (int64_t)r0 * p.lda;
+    const float* __restrict__ sa_p = p.sfa + (int64_t)g * p.sfa_gs + (int64_t)r0 * p.sfa_sm;
+
+    const int e_w = min(wave, A_LOADS - 1);   // this wave's entry of the A-side load list (wave-uniform)
+    uint32_t voff_a;
+    if (e_w < A_SEGS) {
+        const int row = e_w * 8 + rs;
+        voff_a = (uint32_t)min(row, a_rows - 1) * (uint32_t)p.lda + ((pc ^ swz_g(row)) << 4);
+    } else {
+        voff_a = (uint32_t)(min(lane, a_rows - 1) * p.sfa_sm) * 4u;
+    }
+    auto issue_a = [&](int kb, int st) {
+        kb = min(kb, num_kb - 1);
+        const uint32_t lds = a_ring + st * A_STAGE;
+        if (e_w < A_SEGS)
+            dma16_saddr(a_p + (int64_t)kb * kBK, voff_a, lds + e_w * 1024);
+        else
+            dma4_saddr(reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk), voff_a, lds + ROWS * kBK);
+    };
+    auto issue_b = [&](int kb, int st) { S::issue(b_t, voff_b, num_kb, kb, st, wave, smem_lds); };
+    cfloat* sfb_w = (cfloat*)(p.sfb + (int64_t)g * p.sfb_gs +
+                              (int64_t)min((n0 + wave * 32) >> 7, (p.n - 1) >> 7) * p.sfb_sn);
+    float sb_next = sfb_w[0];
+
+    // fragment offsets: row r, logical chunks 2q and 2q + 1 (q = lane >> 4)
+    const int fr = lane & 15, q = lane >> 4;
+    auto frag16 = [&](const uint8_t* tile, int row) {
+        const uint8_t* base = tile + row * 128;
+        const i32x4 lo = *reinterpret_cast<const i32x4*>(base + (((2 * q) ^ swz_g(row)) << 4));
+        const i32x4 hi = *reinterpret_cast<const i32x4*>(base + (((2 * q + 1) ^ swz_g(row)) << 4));
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    f32x4 fin[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) fin[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (!b_primed) {
+        issue_b(0, 0);
+        issue_b(1, 1);
+    }
+#pragma unroll
+    for (int s = 0; s < SA - 1; ++s) issue_a(s, s);
+    wait_vmcnt_barrier<(SA - 2) * 1>();
+    for (int kb = 0; kb < num_kb; ++kb) {
+        issue_a(kb + SA - 1, (kb + SA - 1) % SA);
+        issue_b(kb + 2, (kb + 2) % 3);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* a_tile = smem + S::B_RING + (kb % SA) * A_STAGE;
+        const uint8_t* b_tile = smem + (kb % 3) * S::B_STAGE;
+        const i32x8 oa = frag16(a_tile, fr);
+        const i32x8 ob0 = frag16(b_tile, wave * 32 + fr);
+        const i32x8 ob1 = frag16(b_tile, wave * 32 + 16 + fr);
+        const float sb = sb_next;
+        sb_next = sfb_w[(int64_t)min(kb + 1, num_kb - 1) * p.sfb_sk];
+        const float scl = *reinterpret_cast<const float*>(a_tile + ROWS * kBK + fr * 4) * sb;
+        const f32x4 acc0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ob0, oa, f32x4{}, 0, 0, 0, 0, 0, 0);
+        const f32x4 acc1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ob1, oa, f32x4{}, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            fin[0][e] = __builtin_fmaf(scl, acc0[e], fin[0][e]);
+            fin[1][e] = __builtin_fmaf(scl, acc1[e], fin[1][e]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_barrier<W>();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    // Epilogue: the wave's 16 x 32 block, row-major bf16 through its own 1 KB of
+    // LDS, then one 16-byte store per lane (rows l >> 2, columns 8 (l & 3)..+7).
+    uint8_t* region = smem + wave * 1024;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int col = 16 * h + 4 * q;
+        *reinterpret_cast<uint2*>(region + fr * 64 + col * 2) =
+            uint2{pack_bf16x2(fin[h][0], fin[h][1]), pack_bf16x2(fin[h][2], fin[h][3])};
+    }
+    // (LDS operations of one wave complete in order)
+    const int m = lane >> 2;
+    const uint4 u = *reinterpret_cast<const uint4*>(region + m * 64 + (lane & 3) * 16);
+    const int n = n0 + wave * 32 + (lane & 3) * 8;
+    if (r0 + m < m_g && n < p.n) {
+        uint16_t* dp = static_cast<uint16_t*>(p.d) + (int64_t)g * p.d_gs + (int64_t)(r0 + m) * p.ldd + n;
+        if (n + 8 <= p.n) {
+            *reinterpret_cast<uint4*>(dp) = u;
+        } else {
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (n + e < p.n) dp[e] = static_cast<uint16_t>(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu);
+        }
+    }
+}
+
 template <int NW>
 __global__ void __launch_bounds__(NW * 64, 1)
-fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
+fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles, const int mfma16) {
     static_assert(NW >= 4 && NW <= 8, "4 to 8 waves");
     using S = StreamShape<NW>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
@@ -267,7 +396,8 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
     S::issue(b_t, voff_b, num_kb, 0, 0, wave, smem_lds);
     S::issue(b_t, voff_b, num_kb, 1, 1, wave, smem_lds);
 
-    const int m_g = min(((const __attribute__((address_space(4))) int32_t*)p.layout)[g], p.m);   // masked_m
+    // masked_m (a dense call runs as one group of all p.m rows, layout = null)
+    const int m_g = p.layout ? min(((const __attribute__((address_space(4))) int32_t*)p.layout)[g], p.m) : p.m;
     if (m_g <= 0) {   // uniform over the workgroup; no stage load may outlive it
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return;
@@ -277,6 +407,10 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
         const int a_rows = min(kMR, m_g - r0);
         const int nrt = __builtin_amdgcn_readfirstlane((a_rows + 31) >> 5);
         const bool primed = r0 == 0;
+        if (mfma16 && a_rows <= 16) {
+            masked_pass16<NW>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane);
+            continue;
+        }
         switch (nrt) {
             case 1: masked_pass<NW, 1>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
             case 2: masked_pass<NW, 2>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
@@ -288,14 +422,14 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
 }
 
 template <int NW>
-void launch_nw(const Fp8GemmArgs& a, hipStream_t stream) {
+void launch_nw(const Fp8GemmArgs& a, int mfma16, hipStream_t stream) {
     constexpr int BN = NW * 32;
     const int num_n_tiles = (a.n + BN - 1) / BN;
     const int64_t grid = (int64_t)num_n_tiles * a.num_groups;
     if (grid == 0) return;
     DG_CHECK(grid < (int64_t)1 << 31);
     hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
-                       num_n_tiles);
+                       num_n_tiles, mfma16);
     DG_HIP_CHECK(hipGetLastError());
 }
 
@@ -319,14 +453,16 @@ int fp8_masked_stream_waves(int64_t n, int64_t groups, int cus) {
     return best_nw;
 }
 
-void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& a, int waves, hipStream_t stream) {
+void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& a, int waves, bool mfma16, hipStream_t stream) {
     DG_CHECK(fp8_masked_stream_supported(a));
+    DG_CHECK(a.layout != nullptr || a.num_groups == 1);
+    const int m16 = mfma16 ? 1 : 0;
     switch (waves) {
-        case 4: launch_nw<4>(a, stream); break;
-        case 5: launch_nw<5>(a, stream); break;
-        case 6: launch_nw<6>(a, stream); break;
-        case 7: launch_nw<7>(a, stream); break;
-        case 8: launch_nw<8>(a, stream); break;
+        case 4: launch_nw<4>(a, m16, stream); break;
+        case 5: launch_nw<5>(a, m16, stream); break;
+        case 6: launch_nw<6>(a, m16, stream); break;
+        case 7: launch_nw<7>(a, m16, stream); break;
+        case 8: launch_nw<8>(a, m16, stream); break;
         default: DG_UNSUPPORTED("masked streaming kernel: 4 to 8 waves (block_n 128 to 256 in steps of 32)");
     }
 }

@@ -83,7 +83,8 @@ struct TileConfig {
     int block_m;
     int block_n;
     // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined, 4 = 2 persistent,
-    // 5 = masked weight-streaming (block_m 160 rows per pass, block_n = 32 x waves),
+    // 5 = weight-streaming (block_m 160: 32 x 32 x 64 MFMAs only; 16: passes of at
+    //     most 16 rows on 16 x 16 x 128 MFMAs; block_n = 32 x waves),
     // 6 = 1D1D (block_m 128, block_n = 32 x waves)
     int variant = 1;
 };
@@ -103,11 +104,14 @@ bool fp8_1d2d_v2_tile_supported(int block_m, int block_n);
 
 // The masked weight-streaming kernel (dg_gemm_fp8_masked.hip): K a multiple of
 // 128 (at most 128 blocks), BF16 D without C. `waves` = block_n / 32, 4 to 8.
-// A pass covers kMaskedStreamRows rows of a group.
+// A pass covers kMaskedStreamRows rows of a group. With `mfma16`, a pass of at
+// most 16 rows runs on 16 x 16 x 128 MFMAs (the configuration's block_m is then
+// kStream16Rows). args.layout == null runs a dense call as one group of args.m rows.
 constexpr int kMaskedStreamRows = 160;
+constexpr int kStream16Rows = 16;
 bool fp8_masked_stream_supported(const Fp8GemmArgs& args);
 int fp8_masked_stream_waves(int64_t n, int64_t groups, int cus);
-void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& args, int waves, hipStream_t stream);
+void launch_fp8_gemm_masked_stream(const Fp8GemmArgs& args, int waves, bool mfma16, hipStream_t stream);
 
 // The 1D1D (per-row B scales) kernel, dense or K-grouped (dg_gemm_fp8_1d1d.hip):
 // FP32 D with C, K (each group's K) a multiple of 128; waves 4, 6 or 8.

@@ -369,6 +369,88 @@ def test_masked_stream_equals_pipelined(bn, mn_major):
     assert torch.equal(outs[2].view(torch.int16), outs[5].view(torch.int16))
 
 
+def _masked_call(a, b, d, mm, override=None, expected_m=16):
+    if override:
+        deep_gemm.set_tile_override(override[1], override[2], variant=override[0])
+    try:
+        deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, expected_m=expected_m)
+        return deep_gemm.get_last_config()
+    finally:
+        if override:
+            deep_gemm.set_tile_override(0, 0)
+
+
+@pytest.mark.parametrize('bn', [128, 256])
+def test_masked_mfma16_vs_oracle(bn):
+    """Passes of at most 16 rows on 16 x 16 x 128 MFMAs (block_m 16): the oracle to
+    one BF16 ulp, rows >= masked_m untouched, and within rounding of the
+    32 x 32 x 64 configuration (block_m 160) on the same inputs. masked_m covers
+    0, 1, a partial and a full 16-row pass, 17 (a 32-row pass) and a second pass
+    of 16 rows (176)."""
+    g, max_m, n, k = 6, 192, 320, 1024
+    x = gen.masked_inputs(g, max_m, n, k, seed=60 + bn)
+    x['masked_m'][:] = [0, 1, 7, 16, 17, 176]
+    a_deq = np.stack([oquant.dequant_per_token(x['qa'][i], x['sfa'][i]) for i in range(g)])
+    b_deq = np.stack([oquant.dequant_per_block(x['qb'][i], x['sfb'][i]) for i in range(g)])
+    ref, valid = ogemm.gemm_masked(a_deq, b_deq, x['masked_m'])
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    mm = gen.to_dev(x['masked_m'])
+    outs = {}
+    for bm in (16, 160):
+        d = sentinel_bf16((g, max_m, n))
+        cfg = _masked_call(a, b, d, mm, (5, bm, bn))
+        torch.cuda.synchronize()
+        assert f'block_m={bm} ' in cfg, cfg
+        out = d.float().cpu().numpy()
+        diff, _ = report(f'masked stream block_m={bm} block_n={bn}', out[valid], ref[valid])
+        assert diff < 1e-3
+        tol = np.abs(ref[valid]) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref[valid]).max()
+        assert np.all(np.abs(out[valid] - ref[valid]) <= tol)
+        assert bool((d.view(torch.int16)[torch.from_numpy(~valid).to(DEV)] == SENTINEL).all())
+        outs[bm] = out[valid]
+    # the two MFMA shapes agree to FP32 rounding of the sums
+    assert ogemm.calc_diff(outs[16], outs[160]) < 1e-9
+    # the default configuration for decode-sized groups is block_m 16
+    d = sentinel_bf16((g, max_m, n))
+    cfg = _masked_call(a, b, d, mm, None, expected_m=16)
+    assert ' v5 ' in cfg and 'block_m=16 ' in cfg, cfg
+
+
+@pytest.mark.parametrize('m', [1, 5, 16])
+def test_dense_tiny_m_on_stream_kernel(m):
+    """Dense calls of at most 16 rows run on the weight-streaming kernel's
+    16 x 16 x 128 pass as one group: the oracle, and bitwise equal to a masked
+    call whose group has the same rows."""
+    n, k = 2112, 7168
+    x = gen.dense_inputs(m, n, k, seed=70 + m)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    deep_gemm.fp8_gemm_nt(a, b, d)
+    cfg = deep_gemm.get_last_config()
+    torch.cuda.synchronize()
+    assert ' v5 ' in cfg and 'block_m=16 ' in cfg, cfg
+    out = d.float().cpu().numpy()
+    diff, _ = report(f'dense tiny M={m}', out, ref)
+    assert diff < 1e-3
+    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref).max()
+    assert np.all(np.abs(out - ref) <= tol)
+    # a masked group of the same rows (max_m 32, one group) gives the same bits
+    qa = np.zeros((1, 32, k), np.uint8)
+    qa[0, :m] = x['qa']
+    sfa = np.zeros((1, 32, k // 128), np.float32)
+    sfa[0, :m] = x['sfa']
+    qb = np.empty((1,) + x['qb'].shape, np.uint8)      # (a fresh array: a [None] view has a 0 group stride)
+    qb[0] = x['qb']
+    sfb = np.empty((1,) + x['sfb'].shape, np.float32)
+    sfb[0] = x['sfb']
+    dm = sentinel_bf16((1, 32, n))
+    cfg_m = _masked_call((e4m3(qa), f32(sfa)), (e4m3(qb), f32(sfb)), dm,
+                         gen.to_dev(np.array([m], np.int32)), None, expected_m=m)
+    assert 'block_m=16 ' in cfg_m, cfg_m
+    assert torch.equal(dm[0, :m].view(torch.int16), d.view(torch.int16))
+
+
 # ------------------------------------------------- persistent workgroups (variant 4)
 
 def _with_variant(v, fn):
