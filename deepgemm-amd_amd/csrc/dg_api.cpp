@@ -26,8 +26,10 @@ thread_local std::string t_last_config;
 // Process-wide knobs (the reference keeps them in lazily created singletons,
 // csrc/runtime/runtime.hpp:104, csrc/jit_kernels/heuristics/runtime.hpp:67).
 constexpr int kDefaultMKAlignment = 128;
-// Dense calls of at most this many rows run on the weight-streaming kernel.
-constexpr int kDenseStreamRows = 16;
+// Dense calls of at most this many rows run on the weight-streaming kernel
+// (measured on MI355X over the DeepSeek-V3 (N, K) shapes: faster than every
+// tiled configuration up to 64 rows, slower from 128).
+constexpr int kDenseStreamRows = 64;
 std::atomic<int> g_num_sms{0};                 // 0: query the device
 std::atomic<int> g_mk_alignment{kDefaultMKAlignment};
 std::atomic<int> g_tile_variant{0}, g_tile_m{0}, g_tile_n{0};   // variant 0: heuristic
@@ -420,16 +422,20 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         // run on the streaming kernel as one group (layout null), which loads only
         // the rows that exist (16 x 16 x 128 MFMAs up to 16 rows).
         const bool stream_ok = fp8_masked_stream_supported(args) &&
-                               (kind == kMasked || (kind == kNormal && m_rows <= kDenseStreamRows));
+                               (kind == kMasked || (kind == kNormal && m_rows <= kMaskedStreamRows));
         if (tv == 5) {   // forced: the weight-streaming kernel
             if (!stream_ok)
                 DG_UNSUPPORTED("tile override: the weight-streaming kernel runs the masked layout, or dense calls of at "
                                "most 160 rows, with K % 128 == 0, BF16 D and no C");
             t = {g_tile_m.load(), g_tile_n.load(), 5};
-        } else if (tv == 0 && stream_ok && (kind == kNormal || expected_m <= kMaskedStreamRows)) {
+        } else if (tv == 0 && stream_ok &&
+                   (kind == kNormal ? m_rows <= kDenseStreamRows : expected_m <= kMaskedStreamRows)) {
             // decode-sized groups: the weight-streaming kernel (one pass per group
             // when masked_m <= 160; larger groups take more passes)
-            t = {kStream16Rows, 32 * fp8_masked_stream_waves(n, groups, args.grid_limit), 5};
+            // 16 x 16 x 128 passes for groups of at most 16 rows (5-10% faster there)
+            const int rows_hint = kind == kNormal ? (int)m_rows : expected_m;
+            t = {rows_hint <= kStream16Rows ? kStream16Rows : kMaskedStreamRows,
+                 32 * fp8_masked_stream_waves(n, groups, args.grid_limit), 5};
         } else {
             t = choose_tile_1d2d(kind, m_rows, n, k, kind == kMasked ? groups : 1, align_m);
         }

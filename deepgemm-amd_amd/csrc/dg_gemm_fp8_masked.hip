@@ -20,6 +20,10 @@
 //    after the expert's first workgroup). A(kb + S_A - 1) and B(kb + 2) are
 //    issued before K block kb computes, so two B stages are in flight while a
 //    block computes; B(0) and B(1) are issued before masked_m is even read;
+//  * a block's stage loads are spread over its row-tile iterations (A after
+//    the first MFMA pair, then one B load per iteration) rather than issued in
+//    one burst that would hold every wave at the load queue with the matrix
+//    core idle; B(kb + 2) has two blocks to land, A(kb + 1) all of block kb;
 //  * SFB comes in by scalar loads one K block ahead (no vector-memory count);
 //  * all stage loads are global_load_lds_dwordx4 / _dword with the same
 //    per-wave count, so one s_waitcnt vmcnt immediate serves every wave;
@@ -75,6 +79,15 @@ struct StreamShape {
             const int row = (i * NW + wave) * 8 + rs;
             voff[i] = (uint32_t)min(row, b_rows - 1) * (uint32_t)ldb + ((pc ^ swz_g(row)) << 4);
         }
+    }
+    __device__ static void issue_one(const uint8_t* b_t, const uint32_t (&voff)[LB], int num_kb, int kb, int st,
+                                     int wave, uint32_t smem_lds, int i) {
+        kb = min(kb, num_kb - 1);
+        const uint8_t* base = b_t + (int64_t)kb * kBK;
+        const uint32_t lds = smem_lds + st * B_STAGE + (i * NW + wave) * 1024;
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds), "v"(voff[i]),
+                     "s"(base)
+                     : "memory", "m0");
     }
     __device__ static void issue(const uint8_t* b_t, const uint32_t (&voff)[LB], int num_kb, int kb, int st,
                                  int wave, uint32_t smem_lds) {
@@ -197,8 +210,6 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
     for (int kb = 0; kb < num_kb; ++kb) {
         // The slots refilled here held K block kb - 1, which every wave finished
         // before the last barrier.
-        issue_a(kb + SA - 1, (kb + SA - 1) % SA);
-        issue_b(kb + 2, (kb + 2) % 3);
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* a_tile = smem + S::B_RING + (kb % SA) * A_STAGE;
         const uint8_t* b_tile = smem + (kb % 3) * S::B_STAGE;
@@ -228,6 +239,10 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
                                                                               0);
                 scl[rt & 1] = sa * sb;
             }
+            if (rt == 0) issue_a(kb + SA - 1, (kb + SA - 1) % SA);
+#pragma unroll
+            for (int i = 0; i < LB; ++i)
+                if (min(1 + i, NRT) == rt) S::issue_one(b_t, voff_b, num_kb, kb + 2, (kb + 2) % 3, wave, smem_lds, i);
             if (rt >= 1) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
@@ -373,9 +388,11 @@ __device__ __forceinline__ void masked_pass16(const Fp8GemmArgs& p, uint8_t* sme
     }
 }
 
-template <int NW>
+// M16: passes of at most 16 rows take the 16 x 16 x 128 pass (a separate
+// instantiation, so the 32-row passes keep their register allocation when it is off).
+template <int NW, int M16>
 __global__ void __launch_bounds__(NW * 64, 1)
-fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles, const int mfma16) {
+fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
     static_assert(NW >= 4 && NW <= 8, "4 to 8 waves");
     using S = StreamShape<NW>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
@@ -407,9 +424,11 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles, const 
         const int a_rows = min(kMR, m_g - r0);
         const int nrt = __builtin_amdgcn_readfirstlane((a_rows + 31) >> 5);
         const bool primed = r0 == 0;
-        if (mfma16 && a_rows <= 16) {
-            masked_pass16<NW>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane);
-            continue;
+        if constexpr (M16) {
+            if (a_rows <= 16) {
+                masked_pass16<NW>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane);
+                continue;
+            }
         }
         switch (nrt) {
             case 1: masked_pass<NW, 1>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
@@ -428,8 +447,12 @@ void launch_nw(const Fp8GemmArgs& a, int mfma16, hipStream_t stream) {
     const int64_t grid = (int64_t)num_n_tiles * a.num_groups;
     if (grid == 0) return;
     DG_CHECK(grid < (int64_t)1 << 31);
-    hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
-                       num_n_tiles, mfma16);
+    if (mfma16)
+        hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 1>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
+                           num_n_tiles);
+    else
+        hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 0>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
+                           num_n_tiles);
     DG_HIP_CHECK(hipGetLastError());
 }
 

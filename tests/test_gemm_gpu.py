@@ -451,6 +451,33 @@ def test_dense_tiny_m_on_stream_kernel(m):
     assert torch.equal(dm[0, :m].view(torch.int16), d.view(torch.int16))
 
 
+@pytest.mark.parametrize('m', [17, 33, 64])
+def test_dense_small_m_stream_equals_tiled(m):
+    """Dense calls of 17 to 64 rows run on the weight-streaming kernel's 32 x 32 x 64
+    passes (block_m 160), bitwise equal to the pipelined tiles (same MFMA pair,
+    same per-K-block promotion order) and to the oracle within one BF16 ulp."""
+    n, k = 7168, 2048
+    x = gen.dense_inputs(m, n, k, seed=80 + m)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    deep_gemm.fp8_gemm_nt(a, b, d)
+    cfg = deep_gemm.get_last_config()
+    assert ' v5 ' in cfg and 'block_m=160 ' in cfg, cfg
+    d2 = torch.empty_like(d)
+    deep_gemm.set_tile_override(128, 128, variant=2)
+    try:
+        deep_gemm.fp8_gemm_nt(a, b, d2)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(d.view(torch.int16), d2.view(torch.int16))
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    out = d.float().cpu().numpy()
+    diff, _ = report(f'dense small M={m} (stream)', out, ref)
+    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref).max()
+    assert diff < 1e-3 and np.all(np.abs(out - ref) <= tol)
+
+
 # ------------------------------------------------- persistent workgroups (variant 4)
 
 def _with_variant(v, fn):
