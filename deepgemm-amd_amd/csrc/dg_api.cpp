@@ -745,6 +745,172 @@ void cast_impl(const dg_tensor* x_, const dg_tensor* q_, const dg_tensor* sf_, i
     t_last_config = buf;
 }
 
+// ---------------------------------------------------------------- MoE plumbing
+// The layer around the grouped GEMMs on one GPU, as the reference's MoE baseline
+// runs it (tests/test_mega_moe.py:296-330): dispatch into the grouped layouts,
+// SwiGLU x routing weight -> FP8 (third-party/tilelang_ops/swiglu_apply_weight_to_fp8.py),
+// combine.
+
+bool contiguous_view(const View& t) {
+    int64_t want = 1;
+    for (int i = t.dim() - 1; i >= 0; --i) {
+        if (t.size(i) != 1 && t.stride(i) != want) return false;
+        want *= t.size(i);
+    }
+    return true;
+}
+
+int64_t moe_worst_rows(int64_t tokens, int64_t topk, int64_t experts, int64_t alignment) {
+    return align_up(tokens * topk + experts * (alignment - 1), alignment);
+}
+
+void moe_dispatch_impl(const dg_tensor* x_, const dg_tensor* x_sf_, const dg_tensor* topk_idx_,
+                       const dg_tensor* topk_w_, int32_t num_experts, int32_t layout, int32_t alignment,
+                       const dg_tensor* a_, const dg_tensor* sf_, const dg_tensor* meta_, const dg_tensor* pos_,
+                       const dg_tensor* w_out_, int32_t* workspace, int64_t workspace_ints, hipStream_t stream) {
+    const View x = view(x_, "x"), xs = view(x_sf_, "x_sf"), ti = view(topk_idx_, "topk_idx"), a = view(a_, "a"),
+               sf = view(sf_, "sf"), meta = view(meta_, "grouped_layout"), pos = view(pos_, "pos");
+    DG_CHECK(layout == kMoeContiguous || layout == kMoePsum || layout == kMoeMasked);
+    DG_CHECK(num_experts > 0 && num_experts <= kMoeMaxExperts);
+    DG_CHECK(x.dim() == 2 && x.dtype() == DG_E4M3 && x.stride(-1) == 1 && x.on_device());
+    const int64_t t = x.size(0), kdim = x.size(1), sfk = ceil_div(kdim, (int64_t)128);
+    DG_CHECK(kdim % 16 == 0 && t < ((int64_t)1 << 30));
+    check_vector_alignment(x, "x");
+    DG_CHECK(xs.dim() == 2 && xs.dtype() == DG_F32 && xs.on_device() && xs.size(0) == t && xs.size(1) == sfk);
+    DG_CHECK(ti.dim() == 2 && (ti.dtype() == DG_I32 || ti.dtype() == DG_I64) && ti.on_device() && ti.size(0) == t);
+    const int64_t k = ti.size(1);
+    DG_CHECK(k > 0 && k <= kMoeMaxTopk);
+    if (topk_w_) {
+        const View tw = view(topk_w_, "topk_weights");
+        DG_CHECK(tw.dim() == 2 && tw.dtype() == DG_F32 && tw.on_device() && tw.size(0) == t && tw.size(1) == k);
+    }
+    DG_CHECK(pos.dim() == 2 && pos.dtype() == DG_I32 && pos.on_device() && pos.size(0) == t && pos.size(1) == k &&
+             contiguous_view(pos));
+    DG_CHECK(a.dtype() == DG_E4M3 && a.on_device() && a.stride(-1) == 1 && a.size(-1) == kdim);
+    DG_CHECK(sf.dtype() == DG_F32 && sf.on_device() && sf.size(-1) == sfk);
+    DG_CHECK(meta.dtype() == DG_I32 && meta.on_device() && meta.dim() == 1 && contiguous_view(meta));
+    check_vector_alignment(a, "a");
+    int64_t cap = 0, max_m = 0;
+    if (layout == kMoeMasked) {
+        DG_CHECK(a.dim() == 3 && a.size(0) == num_experts && sf.dim() == 3 && sf.size(0) == num_experts);
+        max_m = a.size(1);
+        DG_CHECK(max_m > 0 && sf.size(1) == max_m && meta.size(0) == num_experts);
+        cap = num_experts * max_m;
+    } else {
+        DG_CHECK(alignment > 0 && alignment % 16 == 0);
+        DG_CHECK(a.dim() == 2 && sf.dim() == 2 && sf.size(0) == a.size(0));
+        cap = a.size(0);
+        // every routing must fit: the segments take at most T*k + E*(alignment - 1) rows
+        DG_CHECK(cap >= moe_worst_rows(t, k, num_experts, alignment));
+        DG_CHECK(meta.size(0) == (layout == kMoeContiguous ? cap : (int64_t)num_experts));
+    }
+    DG_CHECK(cap < ((int64_t)1 << 31));
+    float* w_out = nullptr;
+    if (w_out_) {
+        const View wo = view(w_out_, "row_weights");
+        DG_CHECK(wo.dtype() == DG_F32 && wo.on_device() && contiguous_view(wo));
+        int64_t numel = 1;
+        for (int i = 0; i < wo.dim(); ++i) numel *= wo.size(i);
+        DG_CHECK(numel == cap);
+        w_out = static_cast<float*>(const_cast<void*>(wo.data()));
+    }
+    DG_CHECK(workspace != nullptr && workspace_ints >= moe_dispatch_workspace_ints(t, num_experts));
+    MoeDispatchArgs p{};
+    p.x = static_cast<const uint8_t*>(x.data()), p.ldx = x.stride(0);
+    p.x_sf = static_cast<const float*>(xs.data()), p.sf_st = xs.stride(0), p.sf_sk = xs.stride(1);
+    p.topk = ti.data(), p.topk_i64 = ti.dtype() == DG_I64, p.topk_st = ti.stride(0), p.topk_sk = ti.stride(1);
+    if (topk_w_) {
+        const View tw = view(topk_w_, "topk_weights");
+        p.topk_w = static_cast<const float*>(tw.data()), p.w_st = tw.stride(0), p.w_sk = tw.stride(1);
+    }
+    p.t = (int32_t)t, p.k = (int32_t)k, p.kdim = (int32_t)kdim, p.sfk = (int32_t)sfk;
+    p.num_experts = num_experts, p.layout = layout, p.alignment = alignment, p.max_m = (int32_t)max_m;
+    p.chunks = moe_dispatch_chunks(t);
+    p.a = static_cast<uint8_t*>(const_cast<void*>(a.data()));
+    p.lda = a.stride(-2), p.a_gs = a.dim() == 3 ? a.stride(0) : 0;
+    p.sf = static_cast<float*>(const_cast<void*>(sf.data()));
+    p.sf_sm = sf.stride(-2), p.sf_sk_o = sf.stride(-1), p.sf_gs = sf.dim() == 3 ? sf.stride(0) : 0;
+    p.meta = static_cast<int32_t*>(const_cast<void*>(meta.data()));
+    p.cap_rows = cap;
+    p.w_out = w_out;
+    p.pos = static_cast<int32_t*>(const_cast<void*>(pos.data()));
+    p.ws = workspace;
+    launch_moe_dispatch(p, stream);
+    char buf[160];
+    std::snprintf(buf, sizeof(buf), "moe_dispatch layout=%s experts=%d t=%lld k=%lld kdim=%lld",
+                  layout == kMoeContiguous ? "contiguous" : layout == kMoePsum ? "psum" : "masked", num_experts,
+                  (long long)t, (long long)k, (long long)kdim);
+    t_last_config = buf;
+}
+
+void moe_swiglu_impl(const dg_tensor* x_, const dg_tensor* w_, const dg_tensor* rl_, float clamp, const dg_tensor* q_,
+                     const dg_tensor* sf_, int32_t gran_k, hipStream_t stream) {
+    const View x = view(x_, "x"), q = view(q_, "q"), sf = view(sf_, "sf");
+    DG_CHECK(x.dim() == 2 && x.dtype() == DG_BF16 && x.on_device() && x.stride(-1) == 1);
+    DG_CHECK(q.dim() == 2 && q.dtype() == DG_E4M3 && q.on_device() && q.stride(-1) == 1);
+    DG_CHECK(gran_k == 32 || gran_k == 128);
+    const int64_t m = x.size(0), n = x.size(1) / 2;
+    DG_CHECK(x.size(1) % 2 == 0 && n % gran_k == 0);
+    DG_CHECK(q.size(0) == m && q.size(1) == n);
+    DG_CHECK(sf.dim() == 2 && sf.dtype() == DG_F32 && sf.on_device() && sf.size(0) == m && sf.size(1) == n / gran_k);
+    check_vector_alignment(x, "x");
+    DG_CHECK(reinterpret_cast<uintptr_t>(q.data()) % 8 == 0 && q.stride(0) % 8 == 0);
+    SwigluCastArgs p{};
+    if (w_) {
+        const View w = view(w_, "row_weights");
+        DG_CHECK(w.dtype() == DG_F32 && w.on_device() && contiguous_view(w));
+        int64_t numel = 1;
+        for (int i = 0; i < w.dim(); ++i) numel *= w.size(i);
+        DG_CHECK(numel == m);
+        p.row_weight = static_cast<const float*>(w.data());
+    }
+    if (rl_) {
+        const View rl = view(rl_, "row_layout");
+        DG_CHECK(rl.dtype() == DG_I32 && rl.on_device() && rl.dim() == 1 && rl.size(0) == m && contiguous_view(rl));
+        p.row_layout = static_cast<const int32_t*>(rl.data());
+    }
+    DG_CHECK(m < ((int64_t)1 << 31));
+    p.x = static_cast<const uint16_t*>(x.data()), p.ldx = x.stride(0);
+    p.clamp = clamp;
+    p.q = static_cast<uint8_t*>(const_cast<void*>(q.data())), p.ldq = q.stride(0);
+    p.sf = static_cast<float*>(const_cast<void*>(sf.data())), p.sf_sm = sf.stride(0), p.sf_sk = sf.stride(1);
+    p.m = (int32_t)m, p.n = (int32_t)n, p.gran = gran_k;
+    launch_moe_swiglu_cast(p, stream);
+    char buf[128];
+    std::snprintf(buf, sizeof(buf), "moe_swiglu_cast gran_k=%d m=%lld n=%lld", gran_k, (long long)m, (long long)n);
+    t_last_config = buf;
+}
+
+void moe_combine_impl(const dg_tensor* y_, const dg_tensor* pos_, const dg_tensor* w_, const dg_tensor* out_,
+                      hipStream_t stream) {
+    const View y = view(y_, "y"), pos = view(pos_, "pos"), out = view(out_, "out");
+    DG_CHECK(y.dtype() == DG_BF16 && y.on_device() && y.stride(-1) == 1 && (y.dim() == 2 || y.dim() == 3));
+    DG_CHECK(out.dim() == 2 && out.dtype() == DG_BF16 && out.on_device() && out.stride(-1) == 1);
+    DG_CHECK(pos.dim() == 2 && pos.dtype() == DG_I32 && pos.on_device() && contiguous_view(pos));
+    const int64_t t = pos.size(0), k = pos.size(1), n = y.size(-1);
+    DG_CHECK(out.size(0) == t && out.size(1) == n && n % 8 == 0 && k > 0);
+    check_vector_alignment(y, "y");
+    check_vector_alignment(out, "out");
+    CombineArgs p{};
+    p.y = static_cast<const uint16_t*>(y.data());
+    p.ldy = y.stride(-2);
+    p.y_gs = y.dim() == 3 ? y.stride(0) : 0;
+    p.max_m = y.dim() == 3 ? (int32_t)y.size(1) : 0;
+    p.pos = static_cast<const int32_t*>(pos.data());
+    if (w_) {
+        const View w = view(w_, "topk_weights");
+        DG_CHECK(w.dim() == 2 && w.dtype() == DG_F32 && w.on_device() && w.size(0) == t && w.size(1) == k);
+        p.topk_w = static_cast<const float*>(w.data()), p.w_st = w.stride(0), p.w_sk = w.stride(1);
+    }
+    p.out = static_cast<uint16_t*>(const_cast<void*>(out.data())), p.ldo = out.stride(0);
+    DG_CHECK(t < ((int64_t)1 << 31));
+    p.t = (int32_t)t, p.k = (int32_t)k, p.n = (int32_t)n;
+    launch_moe_combine(p, stream);
+    char buf[128];
+    std::snprintf(buf, sizeof(buf), "moe_combine t=%lld k=%lld n=%lld", (long long)t, (long long)k, (long long)n);
+    t_last_config = buf;
+}
+
 // csrc/apis/gemm.hpp:369-425 (k_grouped_fp8_gemm_nt_contiguous), with
 // check_k_grouped_args (:55-76) and early_return (:17-53).
 void k_grouped_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
@@ -927,6 +1093,44 @@ int dg_plan_sf_transform(const dg_tensor* sf, int32_t mn, int32_t k, const int32
 int dg_per_token_cast_to_fp8(const dg_tensor* x, const dg_tensor* q, const dg_tensor* sf, int32_t gran_k,
                              int32_t use_ue8m0, void* stream) {
     return guarded([&] { cast_impl(x, q, sf, gran_k, use_ue8m0, static_cast<hipStream_t>(stream)); });
+}
+
+int64_t dg_moe_dispatch_workspace_size(int64_t num_tokens, int32_t num_experts) {
+    if (num_tokens < 0 || num_experts <= 0) return -1;
+    return moe_dispatch_workspace_ints(num_tokens, num_experts) * 4;
+}
+
+int64_t dg_moe_dispatch_max_rows(int64_t num_tokens, int32_t num_topk, int32_t num_experts, int32_t alignment) {
+    if (num_tokens < 0 || num_topk <= 0 || num_experts <= 0 || alignment <= 0) return -1;
+    return moe_worst_rows(num_tokens, num_topk, num_experts, alignment);
+}
+
+int dg_moe_dispatch(const dg_tensor* x, const dg_tensor* x_sf, const dg_tensor* topk_idx, const dg_tensor* topk_weights,
+                    int32_t num_experts, int32_t layout, int32_t alignment, const dg_tensor* a, const dg_tensor* sf,
+                    const dg_tensor* grouped_layout, const dg_tensor* pos, const dg_tensor* row_weights,
+                    const dg_tensor* workspace, void* stream) {
+    return guarded([&] {
+        const View ws = view(workspace, "workspace");
+        DG_CHECK(ws.dtype() == DG_I32 && ws.on_device() && contiguous_view(ws));
+        int64_t numel = 1;
+        for (int i = 0; i < ws.dim(); ++i) numel *= ws.size(i);
+        moe_dispatch_impl(x, x_sf, topk_idx, topk_weights, num_experts, layout, alignment, a, sf, grouped_layout, pos,
+                          row_weights, static_cast<int32_t*>(const_cast<void*>(ws.data())), numel,
+                          static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_moe_swiglu_apply_weight_to_fp8(const dg_tensor* x, const dg_tensor* row_weights, const dg_tensor* row_layout,
+                                      float clamp_value, const dg_tensor* q, const dg_tensor* sf, int32_t gran_k,
+                                      void* stream) {
+    return guarded([&] {
+        moe_swiglu_impl(x, row_weights, row_layout, clamp_value, q, sf, gran_k, static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_moe_combine(const dg_tensor* y, const dg_tensor* pos, const dg_tensor* topk_weights, const dg_tensor* out,
+                   void* stream) {
+    return guarded([&] { moe_combine_impl(y, pos, topk_weights, out, static_cast<hipStream_t>(stream)); });
 }
 
 int dg_set_num_sms(int32_t num_sms) {

@@ -183,6 +183,63 @@ struct CastArgs {
 };
 void launch_per_token_cast(const CastArgs& args, hipStream_t stream);
 
+// MoE dispatch / SwiGLU cast / combine (dg_moe.hip).
+constexpr int kMoeMaxExperts = 1024;
+constexpr int kMoeMaxTopk = 16;
+constexpr int kMoeChunkTokens = 64;    // tokens per dispatch chunk (count / scatter workgroup)
+enum MoeLayout : int32_t { kMoeContiguous = 0, kMoePsum = 1, kMoeMasked = 2 };
+struct MoeDispatchArgs {
+    const uint8_t* x;          // e4m3 [t, kdim]
+    int64_t ldx;               // bytes
+    const float* x_sf;         // f32 [t, sfk]
+    int64_t sf_st, sf_sk;
+    const void* topk;          // int32 / int64 [t, k]
+    int32_t topk_i64;
+    int64_t topk_st, topk_sk;
+    const float* topk_w;       // f32 [t, k] or null
+    int64_t w_st, w_sk;
+    int32_t t, k, kdim, sfk, num_experts, layout, alignment, max_m, chunks;
+    uint8_t* a;                // [cap, kdim] or [E, max_m, kdim]
+    int64_t lda, a_gs;         // bytes
+    float* sf;                 // [cap, sfk] or [E, max_m, sfk]
+    int64_t sf_sm, sf_sk_o, sf_gs;
+    int32_t* meta;             // m_indices [cap] / psum ends [E] / masked_m [E]
+    int64_t cap_rows;
+    float* w_out;              // per output row (flattened), or null
+    int32_t* pos;              // [t, k] contiguous
+    int32_t* ws;               // workspace, moe_dispatch_workspace_ints int32
+};
+int moe_dispatch_chunks(int64_t tokens);
+int64_t moe_dispatch_workspace_ints(int64_t tokens, int num_experts);
+void launch_moe_dispatch(const MoeDispatchArgs& args, hipStream_t stream);
+
+struct SwigluCastArgs {
+    const uint16_t* x;         // bf16 [m, 2n]: gate columns [0, n), up columns [n, 2n)
+    int64_t ldx;               // elements
+    const float* row_weight;   // f32 [m] or null
+    const int32_t* row_layout; // int32 [m] (rows with a negative entry get zeros) or null
+    float clamp;               // <= 0: no clamp
+    uint8_t* q;                // e4m3 [m, n]
+    int64_t ldq;
+    float* sf;                 // f32 [m, n / gran], any strides
+    int64_t sf_sm, sf_sk;
+    int32_t m, n, gran;
+};
+void launch_moe_swiglu_cast(const SwigluCastArgs& args, hipStream_t stream);
+
+struct CombineArgs {
+    const uint16_t* y;         // bf16 rows [rows, n] or [E, max_m, n]
+    int64_t ldy, y_gs;         // elements
+    int32_t max_m;             // 0: flat rows; else rows r = e * max_m + i
+    const int32_t* pos;        // [t, k] contiguous
+    const float* topk_w;       // [t, k] or null
+    int64_t w_st, w_sk;
+    uint16_t* out;             // bf16 [t, n]
+    int64_t ldo;
+    int32_t t, k, n;
+};
+void launch_moe_combine(const CombineArgs& args, hipStream_t stream);
+
 // D <- C (or zeros when c is null), used by the K == 0 early return.
 void launch_fill_or_copy(void* d, const void* c, int32_t rows, int32_t cols, int32_t groups,
                          int64_t ldd, int64_t d_gs, int64_t ldc, int64_t c_gs, int elem_bytes,

@@ -451,6 +451,90 @@ def per_token_cast_to_fp8(x: torch.Tensor, use_ue8m0: bool, gran_k: int = 128,
     return q, sf
 
 
+# ------------------------------------------------------------------ MoE plumbing
+
+_MOE_LAYOUTS = {'contiguous': 0, 'psum': 1, 'masked': 2}
+
+
+def _opt(t):
+    return _ref(_desc(t)) if t is not None else None
+
+
+def moe_dispatch(x: Tuple[torch.Tensor, torch.Tensor], topk_idx: torch.Tensor, num_experts: int,
+                 layout: str = 'contiguous', alignment: Optional[int] = None, max_m: Optional[int] = None,
+                 topk_weights: Optional[torch.Tensor] = None):
+    """Token-major FP8 rows -> the expert-grouped layout a grouped GEMM reads, the
+    one-GPU form of DeepEP's expanded / low-latency receive buffers that the
+    reference feeds its grouped GEMMs (tests/test_mega_moe.py:296-310, README.md:78,86).
+
+    x = (e4m3 [T, K], f32 SF [T, ceil(K/128)]); topk_idx [T, topk] (negative ids are
+    not routed). Returns (a, a_sf, grouped_layout, pos, row_weights):
+      contiguous: a [R, K], m_indices [R] (-1 on padding), R = dg_moe_dispatch_max_rows;
+      psum:       a [R, K], psum ends [E];
+      masked:     a [E, max_m, K], masked_m [E] (entries past max_m dropped);
+    pos [T, topk] int32 (row of each (token, slot), masked rows flattened as
+    e * max_m + r, -1 if none); row_weights: the routing weight of each row (None
+    without topk_weights). Deterministic: an expert's rows follow token order."""
+    xq, xs = _pair(x, 'x')
+    if layout not in _MOE_LAYOUTS:
+        raise ValueError(f'layout must be one of {sorted(_MOE_LAYOUTS)}')
+    t, kdim = xq.shape
+    k = topk_idx.shape[1]
+    dev = xq.device
+    alignment = int(alignment or get_mk_alignment_for_contiguous_layout())
+    sfk = (kdim + 127) // 128
+    if layout == 'masked':
+        if not max_m:
+            raise ValueError('the masked layout needs max_m')
+        a = torch.empty((num_experts, max_m, kdim), dtype=torch.float8_e4m3fn, device=dev)
+        a_sf = torch.empty((num_experts, max_m, sfk), dtype=torch.float32, device=dev)
+        gl = torch.empty((num_experts,), dtype=torch.int32, device=dev)
+        rows = num_experts * max_m
+    else:
+        rows = int(_lib.dg_moe_dispatch_max_rows(int(t), int(k), int(num_experts), alignment))
+        _check(0 if rows >= 0 else 1)
+        a = torch.empty((rows, kdim), dtype=torch.float8_e4m3fn, device=dev)
+        a_sf = torch.empty((rows, sfk), dtype=torch.float32, device=dev)
+        gl = torch.empty((rows if layout == 'contiguous' else num_experts,), dtype=torch.int32, device=dev)
+    pos = torch.empty((t, k), dtype=torch.int32, device=dev)
+    w = torch.empty((rows,), dtype=torch.float32, device=dev) if topk_weights is not None else None
+    ws_bytes = int(_lib.dg_moe_dispatch_workspace_size(int(t), int(num_experts)))
+    ws = torch.empty((max(ws_bytes, 4) // 4,), dtype=torch.int32, device=dev)
+    _check(_lib.dg_moe_dispatch(_ref(_desc(xq)), _ref(_desc(xs)), _ref(_desc(topk_idx)), _opt(topk_weights),
+                                int(num_experts), _MOE_LAYOUTS[layout], alignment, _ref(_desc(a)), _ref(_desc(a_sf)),
+                                _ref(_desc(gl)), _ref(_desc(pos)), _opt(w), _ref(_desc(ws)), _ffi.stream_of(xq)))
+    if w is not None and layout == 'masked':
+        w = w.view(num_experts, max_m)
+    return a, a_sf, gl, pos, w
+
+
+def moe_swiglu_apply_weight_to_fp8(x: torch.Tensor, row_weights: Optional[torch.Tensor] = None,
+                                   row_layout: Optional[torch.Tensor] = None, clamp_value: Optional[float] = None,
+                                   gran_k: int = 128) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bf16 [M, 2I] (gate | up, an L1 grouped GEMM's output) -> (e4m3 [M, I], f32 SF
+    [M, I/gran_k]) of y = silu(gate) * up * w: the reference's
+    swiglu_apply_weight_to_fp8 (third-party/tilelang_ops/swiglu_apply_weight_to_fp8.py)
+    with per_token_cast_to_fp8's scale arithmetic, fused in one HBM pass.
+    row_layout (m_indices): rows with a negative entry are written as zeros."""
+    m, i2 = x.shape
+    q = torch.empty((m, i2 // 2), dtype=torch.float8_e4m3fn, device=x.device)
+    sf = torch.empty((m, i2 // 2 // gran_k), dtype=torch.float32, device=x.device)
+    _check(_lib.dg_moe_swiglu_apply_weight_to_fp8(_ref(_desc(x)), _opt(row_weights), _opt(row_layout),
+                                                  float(clamp_value or 0.0), _ref(_desc(q)), _ref(_desc(sf)),
+                                                  int(gran_k), _ffi.stream_of(x)))
+    return q, sf
+
+
+def moe_combine(y: torch.Tensor, pos: torch.Tensor, topk_weights: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16 expert outputs ([R, N] or masked [E, max_m, N]) -> bf16 [T, N]:
+    out[t] = sum over slots of w * y[pos[t, j]] in slot order (w = 1 without
+    topk_weights), the one-GPU form of DeepEP's combine."""
+    out = torch.empty((pos.shape[0], y.shape[-1]), dtype=torch.bfloat16, device=y.device)
+    _check(_lib.dg_moe_combine(_ref(_desc(y)), _ref(_desc(pos)), _opt(topk_weights), _ref(_desc(out)),
+                               _ffi.stream_of(y)))
+    return out
+
+
 def per_token_cast_to_fp8_mn_major(x: torch.Tensor, use_ue8m0: bool,
                                    gran_k: int = 128) -> Tuple[torch.Tensor, torch.Tensor]:
     """per_token_cast_to_fp8 with the scales written straight into the MN-major

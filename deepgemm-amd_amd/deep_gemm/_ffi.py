@@ -80,6 +80,11 @@ SIGNATURES = {
     'dg_get_mn_major_tma_aligned_packed_ue8m0_tensor': (_I, [_T, _T, _V]),
     'dg_plan_sf_transform': (_I, [_T, _I, _I, _P(_I), _P(_I), _I, _I, _I, _P(_I)]),
     'dg_per_token_cast_to_fp8': (_I, [_T, _T, _T, _I, _I, _V]),
+    'dg_moe_dispatch_workspace_size': (ctypes.c_int64, [ctypes.c_int64, _I]),
+    'dg_moe_dispatch_max_rows': (ctypes.c_int64, [ctypes.c_int64, _I, _I, _I]),
+    'dg_moe_dispatch': (_I, [_T, _T, _T, _T, _I, _I, _I, _T, _T, _T, _T, _T, _T, _V]),
+    'dg_moe_swiglu_apply_weight_to_fp8': (_I, [_T, _T, _T, ctypes.c_float, _T, _T, _I, _V]),
+    'dg_moe_combine': (_I, [_T, _T, _T, _T, _V]),
     'dg_k_grouped_fp8_gemm_nt_contiguous': (_I, [_T, _T, _T, _T, _T, _P(_I), _I, _T, _T, _P(_I), _I, _V]),
     'dg_k_grouped_fp8_gemm_tn_contiguous': (_I, [_T, _T, _T, _T, _T, _P(_I), _I, _T, _T, _P(_I), _I, _V]),
     'dg_set_num_sms': (_I, [_I]),

@@ -255,6 +255,75 @@ int dg_plan_sf_transform(const dg_tensor* sf, int32_t mn, int32_t k,
 int dg_per_token_cast_to_fp8(const dg_tensor* x, const dg_tensor* q, const dg_tensor* sf,
                              int32_t gran_k, int32_t use_ue8m0, void* stream);
 
+/* ---------------------------------------------------------------- MoE plumbing */
+
+/* The MoE layer around the grouped GEMMs, for one GPU's experts. The reference
+ * runs it as DeepEP dispatch -> L1 grouped GEMM -> tilelang SwiGLU x routing
+ * weight -> FP8 cast -> L2 grouped GEMM -> DeepEP combine (its non-overlapped
+ * baseline, tests/test_mega_moe.py:296-330; DeepEP itself is not part of the
+ * reference and the exchange between GPUs is not done here). */
+
+/* Bytes of the int32 workspace dg_moe_dispatch needs (-1 on bad arguments). */
+int64_t dg_moe_dispatch_workspace_size(int64_t num_tokens, int32_t num_experts);
+
+/* Rows a contiguous / psum dispatch may use: align(T * topk + E * (alignment - 1),
+ * alignment), the capacity `a` must have (-1 on bad arguments). */
+int64_t dg_moe_dispatch_max_rows(int64_t num_tokens, int32_t num_topk, int32_t num_experts, int32_t alignment);
+
+/* Dispatch: token-major FP8 rows -> the expert-grouped layout of a grouped GEMM,
+ * as DeepEP's expanded (normal) or low-latency (masked) receive buffers feed
+ * m_grouped_fp8_gemm_nt_contiguous / _masked (README.md:78,86). Each (token t,
+ * slot j) with expert e = topk_idx[t, j] in [0, E) gets the next row of e's
+ * segment, in token-then-slot order (deterministic); negative ids are not routed.
+ *   x            e4m3 [T, K], unit stride along K, K % 16 == 0, 16-byte rows
+ *   x_sf         f32 [T, ceil(K/128)], any strides (1 x 128 per-token scales)
+ *   topk_idx     int32 / int64 [T, topk] (topk <= 16), any strides
+ *   topk_weights f32 [T, topk] or null: copied to row_weights
+ *   layout       0 contiguous: `a` [R, K], R >= dg_moe_dispatch_max_rows; segment e
+ *                  starts at a multiple of `alignment` (tests/generators.py:383-407);
+ *                  grouped_layout = int32 m_indices [R], -1 on padding and past the
+ *                  segments; padding rows of a / sf / row_weights are zero
+ *                1 psum: the same rows, grouped_layout = int32 [E] with
+ *                  psum[e] = align(psum[e-1]) + count_e (tests/generators.py:456-461)
+ *                2 masked: `a` [E, max_m, K], rows [0, count_e) of slab e,
+ *                  grouped_layout = masked_m [E] = min(count_e, max_m); entries past
+ *                  max_m are dropped (pos -1); other rows are not written
+ *   sf           f32 [R, ceil(K/128)] or [E, max_m, ceil(K/128)], any strides
+ *   pos          int32 [T, topk] contiguous: the row of (t, j) (masked: e * max_m + r),
+ *                -1 if not routed or dropped
+ *   row_weights  f32 with R (or E * max_m) elements, contiguous, or null
+ *   workspace    int32 device tensor of dg_moe_dispatch_workspace_size bytes
+ * Up to 1024 experts. No synchronization. */
+int dg_moe_dispatch(const dg_tensor* x, const dg_tensor* x_sf, const dg_tensor* topk_idx,
+                    const dg_tensor* topk_weights, int32_t num_experts, int32_t layout, int32_t alignment,
+                    const dg_tensor* a, const dg_tensor* sf, const dg_tensor* grouped_layout, const dg_tensor* pos,
+                    const dg_tensor* row_weights, const dg_tensor* workspace, void* stream);
+
+/* The step between the two grouped GEMMs: y = silu(gate) * up * w, gate = x[:, :I],
+ * up = x[:, I:], then the per-token FP8 cast of y (amax clamped at 1e-4,
+ * sf = amax * fl32(1/448), codes e4m3(y / sf)) - the reference's
+ * swiglu_apply_weight_to_fp8 (third-party/tilelang_ops/swiglu_apply_weight_to_fp8.py:86-120)
+ * with the scale arithmetic of per_token_cast_to_fp8 (deep_gemm/utils/math.py:26-49).
+ *   x            bf16 [M, 2I], unit stride, 16-byte rows; I % gran_k == 0
+ *   row_weights  f32 [M] or null (w = 1)
+ *   row_layout   int32 [M] or null: rows with a negative entry (m_indices padding)
+ *                are written as zeros
+ *   clamp_value  > 0: up clamped to [-c, c] and gate to <= c; <= 0: no clamp
+ *   q            e4m3 [M, I], unit stride, 8-byte rows; sf f32 [M, I/gran_k], any strides
+ *   gran_k       32 or 128 */
+int dg_moe_swiglu_apply_weight_to_fp8(const dg_tensor* x, const dg_tensor* row_weights,
+                                      const dg_tensor* row_layout, float clamp_value, const dg_tensor* q,
+                                      const dg_tensor* sf, int32_t gran_k, void* stream);
+
+/* Combine: out[t] = sum over slots j in order of w[t, j] * y[pos[t, j]] (w = 1 when
+ * topk_weights is null: the weights were applied before the L2 GEMM, as in the
+ * reference's pipeline), each step rounded to f32, the result once to bf16.
+ *   y    bf16 [R, N] or [E, max_m, N] (pos flattened as e * max_m + r), N % 8 == 0
+ *   pos  int32 [T, topk] from dg_moe_dispatch (-1 skipped)
+ *   out  bf16 [T, N] */
+int dg_moe_combine(const dg_tensor* y, const dg_tensor* pos, const dg_tensor* topk_weights, const dg_tensor* out,
+                   void* stream);
+
 /* ---------------------------------------------------------------- knobs */
 
 /* Replace set_num_sms / get_num_sms (csrc/apis/config.hpp:15-20,

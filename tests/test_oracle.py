@@ -343,6 +343,107 @@ def test_psum_rejects_overlapping_groups():
         ogemm.psum_blocks([5, 6], 4)    # group 1 would start at align(5) = 8 > 6
 
 
+@pytest.mark.parametrize('seed', range(4))
+def test_moe_dispatch_against_stable_sort(seed):
+    """oracle.moe.dispatch_rows against an independent construction: a stable
+    sort of the flattened (token, slot) expert ids gives each expert's entries in
+    token-then-slot order; segments start at aligned offsets; psum ends cover
+    exactly the rows oracle.gemm.psum_blocks walks; masked keeps the first max_m
+    entries of each expert."""
+    from oracle import moe as omoe
+    rng = np.random.default_rng(90 + seed)
+    t_n, k, e_n, align = int(rng.integers(1, 40)), int(rng.integers(1, 5)), int(rng.integers(1, 7)), 8
+    idx = rng.integers(-1, e_n, size=(t_n, k))
+    flat = idx.reshape(-1)
+    order = np.argsort(np.where(flat >= 0, flat, e_n), kind='stable')   # not-routed entries last
+    counts = np.array([(flat == e).sum() for e in range(e_n)])
+    starts = np.concatenate([[0], np.cumsum([(c + align - 1) // align * align for c in counts])])[:-1]
+    want = np.full(flat.size, -1)
+    r = 0
+    for e in range(e_n):
+        for i in range(counts[e]):
+            want[order[r]] = starts[e] + i
+            r += 1
+    pos, m_idx, rows = omoe.dispatch_rows(idx, e_n, 'contiguous', align)
+    assert np.array_equal(pos.reshape(-1), want)
+    assert rows == sum((c + align - 1) // align * align for c in counts)
+    assert np.all(starts % align == 0)
+    for e in range(e_n):
+        assert np.all(m_idx[starts[e]:starts[e] + counts[e]] == e)
+    assert (m_idx >= 0).sum() == counts.sum()
+    pos_p, psum, rows_p = omoe.dispatch_rows(idx, e_n, 'psum', align)
+    assert np.array_equal(pos_p, pos) and rows_p == rows
+    covered = {}
+    for g, mb, row_end in ogemm.psum_blocks(psum, align):
+        for row in range(mb * align, min((mb + 1) * align, row_end)):
+            covered[row] = g
+    assert covered == {int(want[i]): int(flat[i]) for i in range(flat.size) if want[i] >= 0}
+    max_m = 3
+    pos_m, mm, _ = omoe.dispatch_rows(idx, e_n, 'masked', max_m=max_m)
+    assert np.array_equal(mm, np.minimum(counts, max_m))
+    for e in range(e_n):
+        ent = [i for i in order[:counts.sum()] if flat[i] == e]
+        for r_, i in enumerate(ent):
+            assert pos_m.reshape(-1)[i] == (e * max_m + r_ if r_ < max_m else -1)
+
+
+def test_moe_dispatch_copies_rows_and_zero_padding():
+    from oracle import moe as omoe
+    rng = np.random.default_rng(5)
+    t_n, k, e_n, kk = 12, 2, 3, 256
+    idx = rng.integers(0, e_n, size=(t_n, k))
+    codes = rng.integers(0, 256, size=(t_n, kk)).astype(np.uint8)
+    sf = rng.random((t_n, 2)).astype(np.float32)
+    w = rng.random((t_n, k)).astype(np.float32)
+    out = omoe.dispatch(codes, sf, idx, e_n, 'contiguous', alignment=8, topk_weights=w)
+    for t in range(t_n):
+        for j in range(k):
+            p = out['pos'][t, j]
+            assert np.array_equal(out['a'][p], codes[t]) and np.array_equal(out['sf'][p], sf[t])
+            assert out['weights'][p] == w[t, j]
+    pad = out['layout'] < 0
+    assert np.all(out['a'][pad] == 0) and np.all(out['sf'][pad] == 0) and np.all(out['weights'][pad] == 0)
+
+
+def test_moe_swiglu_closed_forms():
+    from scipy.special import expit
+    from oracle import moe as omoe
+    rng = np.random.default_rng(6)
+    x = gen_bf16((7, 64), rng)
+    w = rng.random(7)
+    y = omoe.swiglu_apply_weight(x, w)
+    g, u = x[:, :32].astype(np.float64), x[:, 32:].astype(np.float64)
+    assert np.allclose(y, g * expit(g) * u * w[:, None], rtol=1e-14, atol=0)
+    z = omoe.swiglu_apply_weight(np.concatenate([np.zeros((1, 4)), np.full((1, 4), 3.0)], axis=1))
+    assert np.all(z == 0.0)                      # silu(0) = 0
+    c = omoe.swiglu_apply_weight(np.array([[50.0, -50.0, 2.0, 2.0]]), clamp=7.0)
+    assert np.allclose(c, [[7.0 / (1 + np.exp(-7.0)) * 2.0, -50.0 / (1 + np.exp(50.0)) * 2.0]])
+    q, sf = omoe.swiglu_apply_weight_to_fp8(x, w, gran_k=32)
+    qq, ss = oquant.per_token_cast_to_fp8(omoe.swiglu_apply_weight(x, w).astype(np.float32), False, 32)
+    assert np.array_equal(q, qq) and np.array_equal(sf, ss)
+
+
+def test_moe_combine_against_vectorized_sum():
+    from oracle import moe as omoe
+    rng = np.random.default_rng(7)
+    t_n, k, rows, n = 9, 3, 40, 24
+    y = oquant.bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+    pos = rng.integers(-1, rows, size=(t_n, k))
+    w = rng.random((t_n, k)).astype(np.float32)
+    for wts in (None, w):
+        acc = np.zeros((t_n, n), np.float32)
+        for j in range(k):                        # slot order, float32 rounding after each step
+            term = y[np.maximum(pos[:, j], 0)]
+            if wts is not None:
+                term = (wts[:, j:j + 1] * term).astype(np.float32)
+            acc = np.where(pos[:, j:j + 1] >= 0, (acc + term).astype(np.float32), acc)
+        assert np.array_equal(omoe.combine(y, pos, wts), oquant.bf16_round(acc))
+
+
+def gen_bf16(shape, rng):
+    return oquant.bf16_round(rng.standard_normal(shape).astype(np.float32))
+
+
 def test_calc_diff_closed_forms():
     x = np.random.default_rng(12).standard_normal(1000)
     assert ogemm.calc_diff(x, x) == pytest.approx(0.0, abs=1e-15)
