@@ -1120,6 +1120,27 @@ int dg_moe_dispatch(const dg_tensor* x, const dg_tensor* x_sf, const dg_tensor* 
     });
 }
 
+int dg_moe_dispatch_noalloc(const dg_tensor* x, const dg_tensor* x_sf, const dg_tensor* topk_idx,
+                            const dg_tensor* topk_weights, int32_t num_experts, int32_t layout, int32_t alignment,
+                            const dg_tensor* a, const dg_tensor* sf, const dg_tensor* grouped_layout,
+                            const dg_tensor* pos, const dg_tensor* row_weights, void* stream) {
+    return guarded([&] {
+        const View xv = view(x, "x");
+        DG_CHECK(xv.dim() == 2 && num_experts > 0);
+        int dev = -1;   // the scratch used is the current device's copy
+        DG_HIP_CHECK(hipGetDevice(&dev));
+        DG_CHECK(xv.on_device() && x->device == dev);
+        const int64_t need = moe_dispatch_workspace_ints(xv.size(0), num_experts);
+        if (need > kMoeScratchInts)
+            throw Error(DG_ERR_INVALID, "Assertion", __FILE__, __LINE__,
+                        "the allocation-free dispatch needs " + std::to_string(need) +
+                            " int32 of scratch, more than its fixed " + std::to_string(kMoeScratchInts) +
+                            "; use dg_moe_dispatch with a workspace");
+        moe_dispatch_impl(x, x_sf, topk_idx, topk_weights, num_experts, layout, alignment, a, sf, grouped_layout, pos,
+                          row_weights, moe_scratch_device_ptr(), kMoeScratchInts, static_cast<hipStream_t>(stream));
+    });
+}
+
 int dg_moe_swiglu_apply_weight_to_fp8(const dg_tensor* x, const dg_tensor* row_weights, const dg_tensor* row_layout,
                                       float clamp_value, const dg_tensor* q, const dg_tensor* sf, int32_t gran_k,
                                       void* stream) {

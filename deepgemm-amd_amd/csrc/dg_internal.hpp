@@ -209,6 +209,11 @@ struct MoeDispatchArgs {
     int32_t* pos;              // [t, k] contiguous
     int32_t* ws;               // workspace, moe_dispatch_workspace_ints int32
 };
+// The allocation-free dispatch: a file-scope device array of kMoeScratchInts
+// int32 (1 MiB) per GPU; the device address of the current GPU's copy.
+constexpr int64_t kMoeScratchInts = 262144;
+constexpr int kMoeMaxDevices = 64;
+int32_t* moe_scratch_device_ptr();
 int moe_dispatch_chunks(int64_t tokens);
 int64_t moe_dispatch_workspace_ints(int64_t tokens, int num_experts);
 void launch_moe_dispatch(const MoeDispatchArgs& args, hipStream_t stream);

@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "dg_internal.hpp"
 
@@ -303,7 +304,30 @@ __global__ void __launch_bounds__(kThreads) moe_combine_kernel(const CombineArgs
     *reinterpret_cast<uint4*>(p.out + (int64_t)t * p.ldo + col) = uint4{o[0], o[1], o[2], o[3]};
 }
 
+// Scratch of the dispatch entry point that allocates nothing: the workspace of
+// one call (per-chunk expert counts, starts, totals), kMoeScratchInts int32 on
+// each GPU the library runs on, held until the process ends. Host code must not
+// pass `scratch` itself (a host-side stand-in): it passes the device address
+// that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) int32_t scratch[kMoeScratchInts];
+
 }  // namespace
+
+int32_t* moe_scratch_device_ptr() {
+    static std::mutex mu;
+    static int32_t* ptrs[kMoeMaxDevices] = {};
+    int dev = -1;
+    DG_HIP_CHECK(hipGetDevice(&dev));
+    DG_CHECK(dev >= 0 && dev < kMoeMaxDevices);
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[dev] == nullptr) {   // once per device, with that device current
+        void* p = nullptr;
+        DG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        DG_CHECK(p != nullptr);
+        ptrs[dev] = static_cast<int32_t*>(p);
+    }
+    return ptrs[dev];
+}
 
 int moe_dispatch_chunks(int64_t tokens) { return (int)((tokens + kMoeChunkTokens - 1) / kMoeChunkTokens); }
 

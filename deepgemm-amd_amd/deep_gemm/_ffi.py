@@ -83,6 +83,7 @@ SIGNATURES = {
     'dg_moe_dispatch_workspace_size': (ctypes.c_int64, [ctypes.c_int64, _I]),
     'dg_moe_dispatch_max_rows': (ctypes.c_int64, [ctypes.c_int64, _I, _I, _I]),
     'dg_moe_dispatch': (_I, [_T, _T, _T, _T, _I, _I, _I, _T, _T, _T, _T, _T, _T, _V]),
+    'dg_moe_dispatch_noalloc': (_I, [_T, _T, _T, _T, _I, _I, _I, _T, _T, _T, _T, _T, _V]),
     'dg_moe_swiglu_apply_weight_to_fp8': (_I, [_T, _T, _T, ctypes.c_float, _T, _T, _I, _V]),
     'dg_moe_combine': (_I, [_T, _T, _T, _T, _V]),
     'dg_k_grouped_fp8_gemm_nt_contiguous': (_I, [_T, _T, _T, _T, _T, _P(_I), _I, _T, _T, _P(_I), _I, _V]),

@@ -299,6 +299,19 @@ int dg_moe_dispatch(const dg_tensor* x, const dg_tensor* x_sf, const dg_tensor* 
                     const dg_tensor* a, const dg_tensor* sf, const dg_tensor* grouped_layout, const dg_tensor* pos,
                     const dg_tensor* row_weights, const dg_tensor* workspace, void* stream);
 
+/* dg_moe_dispatch without the workspace argument: it allocates nothing. No
+ * counterpart in the reference; it is for callers that cannot allocate (HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Its workspace is
+ * a fixed 1 MiB device array in the library (262144 int32 per GPU, held until the
+ * process ends), enough for num_experts * ceil(num_tokens / 64) + 2 * num_experts + 1
+ * int32 (e.g. 65000 tokens over 256 experts); larger calls fail with
+ * DG_ERR_INVALID. Every call on one GPU shares that array, so calls that overlap
+ * on one GPU (two streams at once) race. Results equal dg_moe_dispatch's. */
+int dg_moe_dispatch_noalloc(const dg_tensor* x, const dg_tensor* x_sf, const dg_tensor* topk_idx,
+                            const dg_tensor* topk_weights, int32_t num_experts, int32_t layout, int32_t alignment,
+                            const dg_tensor* a, const dg_tensor* sf, const dg_tensor* grouped_layout,
+                            const dg_tensor* pos, const dg_tensor* row_weights, void* stream);
+
 /* The step between the two grouped GEMMs: y = silu(gate) * up * w, gate = x[:, :I],
  * up = x[:, I:], then the per-token FP8 cast of y (amax clamped at 1e-4,
  * sf = amax * fl32(1/448), codes e4m3(y / sf)) - the reference's
