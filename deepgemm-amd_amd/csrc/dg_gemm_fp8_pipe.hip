@@ -19,6 +19,9 @@
 //    loads for kb: once every wave passes it, the stage is complete and every
 //    wave has consumed the slot about to be refilled. (The usual __syncthreads()
 //    also drains every later stage's loads, which would serialize the ring.)
+//    Two-stage dense, masked and psum tiles add a second barrier at the top of
+//    each block that frees the stage's B side early (SPLIT below), so each
+//    barrier releases half a stage of loads.
 //  * LDS rows are 128 bytes; 16-byte chunk c of row r sits at c ^ g(r) with
 //    g(r) = ((r >> 1) ^ ((r & 1) << 2)) & 7: 16 consecutive rows at one logical
 //    chunk hit distinct banks for 8- and 16-lane LDS phases alike. A lane of the
@@ -295,22 +298,29 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
         const int ks = kb + 1;
         issue_segment(min(ks / (KSA ? KSA : 1) + 1, ksa_last), ks % (KSA ? KSA : 1), false);
     };
-    auto issue_stage = [&](int kb, int st) {
+    // part: 0 = the whole stage, 1 = the A side (A rows and SFA), 2 = the B side
+    // (a literal at every call, folded away once the lambda is inlined)
+    auto issue_stage = [&](int kb, int st, int part = 0) {
         const uint32_t stage_lds = smem_lds + st * STAGE_BYTES;
         if constexpr (!KT) {
             const uint8_t* a_kb = a_base + (int64_t)kb * kBK;
             const uint8_t* b_kb = b_base + (int64_t)kb * kBK;
+            if (part != 2) {
 #pragma unroll
             for (int i = 0; i < A_INSTR; ++i) {
                 const int seg = i * NW + wave;
                 dma16_saddr(a_kb, clamped_voff(seg, a_rows, lda), stage_lds + seg * 1024);
             }
+            }
+            if (part != 1) {
 #pragma unroll
             for (int i = 0; i < B_INSTR; ++i) {
                 const int seg = i * NW + wave;
                 dma16_saddr(b_kb, clamped_voff(seg, b_rows, ldb), stage_lds + BM * kBK + seg * 1024);
             }
+            }
             if constexpr (!KSA)
+                if (part != 2)
                 dma4_saddr(reinterpret_cast<const uint8_t*>(sa_base + (int64_t)kb * p.sfa_sk), voff_sa,
                            stage_lds + SA_OFF + wave * 256);
             if constexpr (SB1D)
@@ -407,9 +417,22 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // remain in flight (vector loads retire in order).
     // (With two stages the count is always 0; a branch here would split the
     // unrolled MFMA sequence and wreck register allocation.)
+    // SPLIT (two stages): a stage's B side is consumed as soon as the B
+    // fragments of its block are in registers, which every wave reads at the end
+    // of the previous block, while its A side is read slice by slice until the
+    // hand-off. So the B side of stage kb + 2 is issued at the top of block kb,
+    // after a barrier that certifies those reads, and only the A side at the
+    // hand-off: each hand-off then queues half the loads (a wave blocked on a
+    // full load queue issues no MFMA either), and B gets most of two blocks to
+    // land. At the hand-off the B side of stage kb + 2 (and the block's
+    // scale-group load) may stay in flight. (Contiguous and persistent tiles
+    // keep the single hand-off: with the extra barrier they spill registers.)
+    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D && !PERSIST && KIND != kContiguous;
     auto wait_stage = [&](int s) {
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (STAGES == 2) {
+        if constexpr (SPLIT) {
+            wait_vmcnt_barrier<B_INSTR + (KSA ? 1 : 0)>();
+        } else if constexpr (STAGES == 2) {
             wait_vmcnt_barrier<KSA ? 1 : 0>();   // (KSA: the block's segment load stays in flight)
         } else {
             if (s + STAGES - 2 < num_kb)
@@ -454,9 +477,23 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     for (int kb = 0; kb < num_kb; ++kb) {
         if constexpr (KSA) issue_block_segment(kb);
         if (!wave_computes) {
-            wait_stage(kb + 1);
-            issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES);
+            if constexpr (SPLIT) {
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES, 2);
+                wait_stage(kb + 1);
+                issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES, 1);
+            } else {
+                wait_stage(kb + 1);
+                issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES);
+            }
         } else {
+        if constexpr (SPLIT) {
+            // every wave's B fragment reads of block kb (issued at the end of the
+            // previous block) have returned: the B side of this slot is free.
+            // (No scheduling barriers here: they cost registers in the K loop.)
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES, 2);
+        }
         load_scales(kb);
         const uint8_t* a_tile = smem + (kb % STAGES) * STAGE_BYTES;
         const uint8_t* next = smem + ((kb + 1) % STAGES) * STAGE_BYTES;
@@ -472,7 +509,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                 // (the index is clamped rather than branched on: a branch here costs
                 // registers. Past the last block this re-loads the last stage into the
                 // free slot; nothing reads it.)
-                issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES);
+                issue_stage(min(kb + STAGES, num_kb - 1), kb % STAGES, SPLIT ? 1 : 0);
                 opA[0][0] = frag(next, wm * WM, 0);
                 opA[0][1] = frag(next, wm * WM, 1);
             }
