@@ -30,6 +30,20 @@ constexpr int kDefaultMKAlignment = 128;
 // (measured on MI355X over the DeepSeek-V3 (N, K) shapes: faster than every
 // tiled configuration up to 64 rows, slower from 128).
 constexpr int kDenseStreamRows = 64;
+// Dense calls of at most 16 rows take the tiny-M kernel (K split over a
+// workgroup's waves, N / 16 or N / 32 workgroups) unless the streaming kernel
+// already has this many workgroups (N >= 8192 or so); measured on MI355X at
+// M = 1 and 16: 1.2-2.6x faster for N <= 7168, slower at N = 24576 and 32768.
+constexpr int kTinyMStreamGrid = 64;
+
+// Tiny-M configuration (measured): 8 waves when the rows are few and each wave
+// gets at least 4 K blocks, else 4 (fewer workgroup-wide A re-reads per K
+// block); 32 columns per workgroup once N / 16 exceeds the CU count, else 16.
+TileConfig choose_tinym(int64_t m, int64_t n, int64_t k) {
+    const int waves_variant = (m <= 4 && k / 128 >= 32) ? 8 : 9;
+    const int cols = n > 4096 ? 32 : 16;
+    return TileConfig{kTinyMRows, cols, waves_variant};
+}
 std::atomic<int> g_num_sms{0};                 // 0: query the device
 std::atomic<int> g_mk_alignment{kDefaultMKAlignment};
 std::atomic<int> g_tile_variant{0}, g_tile_m{0}, g_tile_n{0};   // variant 0: heuristic
@@ -423,7 +437,20 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         // the rows that exist (16 x 16 x 128 MFMAs up to 16 rows).
         const bool stream_ok = fp8_masked_stream_supported(args) &&
                                (kind == kMasked || (kind == kNormal && m_rows <= kMaskedStreamRows));
-        if (tv == 5) {   // forced: the weight-streaming kernel
+        // Dense calls of at most 16 rows: K split over the waves of a workgroup, so
+        // the launch has N / 16 workgroups instead of the streaming kernel's N / 128.
+        const bool tinym_ok = kind == kNormal && fp8_tinym_supported(args);
+        if (tv == 8 || tv == 9) {   // forced: the tiny-M kernel
+            if (!tinym_ok)
+                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 16 rows with "
+                               "K % 128 == 0, BF16 D and no C");
+            t = {kTinyMRows, g_tile_n.load(), tv};
+        } else if (tv == 0 && tinym_ok &&
+                   (!stream_ok || (n + 32 * fp8_masked_stream_waves(n, 1, args.grid_limit) - 1) /
+                                          (32 * fp8_masked_stream_waves(n, 1, args.grid_limit)) <
+                                      kTinyMStreamGrid)) {
+            t = choose_tinym(m_rows, n, k);
+        } else if (tv == 5) {   // forced: the weight-streaming kernel
             if (!stream_ok)
                 DG_UNSUPPORTED("tile override: the weight-streaming kernel runs the masked layout, or dense calls of at "
                                "most 160 rows, with K % 128 == 0, BF16 D and no C");
@@ -442,7 +469,9 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
-        if (t.variant == 5)
+        if (t.variant == 8 || t.variant == 9)
+            launch_fp8_gemm_tinym(args, t.variant == 8 ? 8 : 4, t.block_n, stream);
+        else if (t.variant == 5)
             launch_fp8_gemm_masked_stream(args, t.block_n / 32, t.block_m == kStream16Rows, stream);
         else if (t.variant >= 2)
             launch_fp8_gemm_1d2d_v2(kind, t, args, stream);
@@ -1197,6 +1226,8 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
                                           block_n <= 256)
                         : variant == 6 ? (block_m == 128 && (block_n == 128 || block_n == 192 || block_n == 256))
                         : variant == 7 ? (block_m == 256 && block_n == 128)
+                        : variant == 8 || variant == 9
+                            ? (block_m == kTinyMRows && (block_n == 16 || block_n == 32 || block_n == 64))
                                        : (variant == 4 && block_m == 256 && block_n == 256);
         if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;

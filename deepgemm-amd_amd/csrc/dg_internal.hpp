@@ -85,9 +85,17 @@ struct TileConfig {
     // FP32-scale kernels: 1 = register-staged, 2 = LDS-pipelined, 4 = 2 persistent,
     // 5 = weight-streaming (block_m 160: 32 x 32 x 64 MFMAs only; 16: passes of at
     //     most 16 rows on 16 x 16 x 128 MFMAs; block_n = 32 x waves),
-    // 6 = 1D1D (block_m 128, block_n = 32 x waves)
+    // 6 = 1D1D (block_m 128, block_n = 32 x waves),
+    // 8 / 9 = dense tiny M with 8 / 4 waves (block_m 16, block_n 16, 32 or 64
+    //     columns per workgroup: K split over the waves of a workgroup)
     int variant = 1;
 };
+
+// Dense calls of at most 16 rows with K split over the waves of a workgroup
+// (dg_gemm_fp8_tinym.hip): M <= 16, K % 128 == 0, BF16 D, no C.
+constexpr int kTinyMRows = 16;
+bool fp8_tinym_supported(const Fp8GemmArgs& a);
+void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream);
 
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
 // Throws dgm::Error on unsupported configurations or launch failures.

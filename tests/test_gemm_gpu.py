@@ -418,16 +418,20 @@ def test_masked_mfma16_vs_oracle(bn):
 
 @pytest.mark.parametrize('m', [1, 5, 16])
 def test_dense_tiny_m_on_stream_kernel(m):
-    """Dense calls of at most 16 rows run on the weight-streaming kernel's
-    16 x 16 x 128 pass as one group: the oracle, and bitwise equal to a masked
-    call whose group has the same rows."""
+    """Dense calls of at most 16 rows forced onto the weight-streaming kernel's
+    16 x 16 x 128 pass run as one group: the oracle, and bitwise equal to a
+    masked call whose group has the same rows."""
     n, k = 2112, 7168
     x = gen.dense_inputs(m, n, k, seed=70 + m)
     ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
     d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
-    deep_gemm.fp8_gemm_nt(a, b, d)
-    cfg = deep_gemm.get_last_config()
+    deep_gemm.set_tile_override(16, 128, variant=5)
+    try:
+        deep_gemm.fp8_gemm_nt(a, b, d)
+        cfg = deep_gemm.get_last_config()
+    finally:
+        deep_gemm.set_tile_override(0, 0, variant=0)
     torch.cuda.synchronize()
     assert ' v5 ' in cfg and 'block_m=16 ' in cfg, cfg
     out = d.float().cpu().numpy()
@@ -449,6 +453,45 @@ def test_dense_tiny_m_on_stream_kernel(m):
                          gen.to_dev(np.array([m], np.int32)), None, expected_m=m)
     assert 'block_m=16 ' in cfg_m, cfg_m
     assert torch.equal(dm[0, :m].view(torch.int16), d.view(torch.int16))
+
+
+@pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (5, 2112, 7168), (16, 7168, 2048), (3, 104, 384),
+                                   (16, 24576, 1536), (7, 4096, 16384), (1, 576, 128)])
+def test_dense_tiny_m_split_k_kernel(m, n, k):
+    """The tiny-M kernel (K split over the waves of a workgroup, partial sums
+    added in wave order), in each of its configurations (8 or 4 waves; 16, 32 or
+    64 columns per workgroup): the oracle within one BF16 ulp plus the FP32
+    accumulation bound, ragged N (104, not a multiple of 16 or 32), fewer K
+    blocks than waves (K = 128, 384), MN-major SFA equal to K-major, and
+    bitwise-identical reruns. The default routing takes it for N up to 7168."""
+    x = gen.dense_inputs(m, n, k, seed=90 + m + n)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    sfa_mn = deep_gemm.get_mn_major_tma_aligned_tensor(a[1])
+    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref).max()
+    for v, bn in ((8, 16), (9, 16), (8, 32), (9, 32), (8, 64), (9, 64), (0, 0)):
+        deep_gemm.set_tile_override(16 if v else 0, bn, variant=v)
+        try:
+            d = sentinel_bf16((m, n))
+            deep_gemm.fp8_gemm_nt(a, b, d)
+            cfg = deep_gemm.get_last_config()
+            d2 = torch.empty_like(d)
+            deep_gemm.fp8_gemm_nt((a[0], sfa_mn), b, d2)
+            for _ in range(5):
+                deep_gemm.fp8_gemm_nt(a, b, d)
+        finally:
+            deep_gemm.set_tile_override(0, 0)
+        torch.cuda.synchronize()
+        print(f'  {cfg}', flush=True)
+        if v:
+            assert f' v{v} ' in cfg and f'block_n={bn} ' in cfg, cfg
+        elif n <= 7168:
+            assert ' v8 ' in cfg or ' v9 ' in cfg, cfg
+        out = d.float().cpu().numpy()
+        diff, _ = report(f'dense tiny M={m} N={n} K={k} [{cfg.split(" kind")[0]} {bn}]', out, ref)
+        assert diff < 1e-3
+        assert np.all(np.abs(out - ref) <= tol)
+        assert torch.equal(d2.view(torch.int16), d.view(torch.int16))
 
 
 @pytest.mark.parametrize('m', [17, 33, 64])
