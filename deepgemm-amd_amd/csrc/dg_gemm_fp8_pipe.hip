@@ -425,9 +425,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // hand-off: each hand-off then queues half the loads (a wave blocked on a
     // full load queue issues no MFMA either), and B gets most of two blocks to
     // land. At the hand-off the B side of stage kb + 2 (and the block's
-    // scale-group load) may stay in flight. (Contiguous and persistent tiles
-    // keep the single hand-off: with the extra barrier they spill registers.)
-    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D && !PERSIST && KIND != kContiguous;
+    // scale-group load) may stay in flight. (Persistent tiles, and contiguous
+    // ones without 4-block scale groups, keep the single hand-off: with the extra
+    // barrier they spill registers.)
+    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D && !PERSIST && (KIND != kContiguous || KSA == 4);
     auto wait_stage = [&](int s) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (SPLIT) {
@@ -652,22 +653,18 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
     const dim3 gdim(static_cast<unsigned>(grid)), bdim(WGM * WGN * 64);
     const bool k_tail = (a.k % kBK) != 0;
-    // K-major SFA scale groups (one 16- or 32-byte load of a row's scales per 4 or 8 K blocks)
+    // K-major SFA scale groups (one 16-byte load of a row's scales per 4 K blocks).
+    // The kernel also takes groups of 8 (32 bytes); with the split hand-off the
+    // groups of 4 measured faster (dense 929 against 952 us over the config-2
+    // shapes, and the contiguous kernel spills with 8).
     constexpr bool KSA_OK = STAGES == 2 && !PERSIST && (KIND == kNormal || KIND == kContiguous);
     const bool kmajor = KSA_OK && a.sfa_sk == 1 && a.sfa_sm % 4 == 0 && (reinterpret_cast<uintptr_t>(a.sfa) & 15) == 0;
-    const int ksa = !kmajor || a.k > kMaxKBlocksKsa * kBK ? 0
-                    : a.k % (8 * kBK) == 0                ? 8
-                    : a.k % (4 * kBK) == 0                ? 4
-                                                          : 0;
+    const int ksa = !kmajor || a.k > kMaxKBlocksKsa * kBK ? 0 : a.k % (4 * kBK) == 0 ? 4 : 0;
 #define DG_PIPE_LAUNCH(OF, HC)                                                                                       \
     do {                                                                                                             \
         if (k_tail)                                                                                                  \
             hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 1, PERSIST>), gdim, \
                                bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
-        else if (ksa == 8)                                                                                           \
-            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST, 0,        \
-                                                          KSA_OK ? 8 : 0>),                                          \
-                               gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                    \
         else if (ksa == 4)                                                                                           \
             hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST, 0,        \
                                                           KSA_OK ? 4 : 0>),                                          \

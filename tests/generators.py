@@ -92,3 +92,15 @@ def to_dev(x: np.ndarray, dtype=None, device='cuda'):
     if dtype is not None and t.dtype != dtype:
         t = t.view(dtype)
     return t.to(device)
+
+
+def dense_call_same_order(deep_gemm, a, b, d):
+    """fp8_gemm_nt on the pipelined 256 x 256 tile, whose MFMA pair and per-K-block
+    promotion order every grouped kernel shares, so a contiguous segment or a masked
+    expert must equal it bit for bit. (By default a dense call of at most 16 rows
+    takes the tiny-M kernel, which groups the K sum differently.)"""
+    deep_gemm.set_tile_override(256, 256, variant=2)
+    try:
+        deep_gemm.fp8_gemm_nt(a, b, d)
+    finally:
+        deep_gemm.set_tile_override(0, 0)

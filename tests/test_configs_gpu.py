@@ -28,6 +28,7 @@ import bench
 import deep_gemm
 from oracle import gemm as ogemm
 from oracle import quant as oquant
+import generators as gen
 
 pytestmark = pytest.mark.gpu
 
@@ -198,7 +199,7 @@ def test_cfg3_contiguous(contiguous_ops, idx):
     for e in {max(nonempty, key=lambda i: ms[i]), min(nonempty, key=lambda i: ms[i])}:
         s, mi = int(starts[e]), ms[e]
         dd = torch.empty((mi, n), dtype=torch.bfloat16, device=DEV)
-        deep_gemm.fp8_gemm_nt((op['a'][0][s:s + mi], op['a'][1][s:s + mi]), (bq[e], bs[e]), dd)
+        gen.dense_call_same_order(deep_gemm, (op['a'][0][s:s + mi], op['a'][1][s:s + mi]), (bq[e], bs[e]), dd)
         assert torch.equal(dd.view(torch.int16), d[s:s + mi].view(torch.int16)), f'segment {e}'
     rerun_identical(call, d)
 
@@ -247,7 +248,7 @@ def test_cfg4_masked(masked_ops, idx):
     for e in (0, g - 1):
         mm = int(masked[e])
         dd = torch.empty((mm, n), dtype=torch.bfloat16, device=DEV)
-        deep_gemm.fp8_gemm_nt((aq[e][:mm], as_[e][:mm]), (bq[e], bs[e]), dd)
+        gen.dense_call_same_order(deep_gemm, (aq[e][:mm], as_[e][:mm]), (bq[e], bs[e]), dd)
         assert torch.equal(dd.view(torch.int16), d[e, :mm].view(torch.int16)), f'expert {e}'
     rerun_identical(call, d)
 

@@ -155,8 +155,8 @@ def test_dense_determinism_and_bounds():
 def test_mn_major_sfa_equals_k_major(tile, m, n, k):
     """SFA in the reference's MN-major TMA-aligned layout gives the same bits as K-major SFA.
     With two-stage tiles, K-major SFA is read through the kernel's scale groups of
-    8 K blocks (K % 1024 == 0) or 4 (K % 512 == 0; K = 1408 keeps the per-stage
-    loads), and each case is checked against the oracle as well."""
+    4 K blocks (K % 512 == 0; K = 1408 keeps the per-stage loads), and each case
+    is checked against the oracle as well."""
     x = gen.dense_inputs(m, n, k, seed=4)
     a_t, b = e4m3(x['qa']), (e4m3(x['qb']), f32(x['sfb']))
     sfa = f32(x['sfa'])
@@ -241,7 +241,7 @@ def _contiguous_case(ms, aligned, n, k):
     for i, (mi_, ai) in enumerate(zip(ms, aligned)):
         if mi_ > 0:
             dd = torch.empty((mi_, n), dtype=torch.bfloat16, device=DEV)
-            deep_gemm.fp8_gemm_nt((a[0][start:start + mi_], a[1][start:start + mi_]), (b[0][i], b[1][i]), dd)
+            gen.dense_call_same_order(deep_gemm, (a[0][start:start + mi_], a[1][start:start + mi_]), (b[0][i], b[1][i]), dd)
             assert torch.equal(dd.view(torch.int16), d[start:start + mi_].view(torch.int16)), f'segment {i}'
         start += ai
     # determinism
@@ -291,7 +291,7 @@ def test_psum_layout():
             s, e = starts[i], ends[i]
             if e > s:
                 dd = torch.empty((e - s, n), dtype=torch.bfloat16, device=DEV)
-                deep_gemm.fp8_gemm_nt((a[0][s:e], a[1][s:e]), (b[0][i], b[1][i]), dd)
+                gen.dense_call_same_order(deep_gemm, (a[0][s:e], a[1][s:e]), (b[0][i], b[1][i]), dd)
                 assert torch.equal(dd.view(torch.int16), d[s:e].view(torch.int16)), f'group {i}'
             pe = (e + align - 1) // align * align
             if zero_pad and pe > e:
@@ -321,7 +321,7 @@ def test_masked_vs_oracle(n, k):
     for i in range(g):
         r = int(x['masked_m'][i])
         dd = torch.empty((r, n), dtype=torch.bfloat16, device=DEV)
-        deep_gemm.fp8_gemm_nt((a[0][i, :r], a[1][i, :r]), (b[0][i], b[1][i]), dd)
+        gen.dense_call_same_order(deep_gemm, (a[0][i, :r], a[1][i, :r]), (b[0][i], b[1][i]), dd)
         assert torch.equal(dd.view(torch.int16), d[i, :r].view(torch.int16))
 
 

@@ -31,6 +31,7 @@ import torch
 import deep_gemm
 from oracle import gemm as ogemm
 from oracle import quant as oquant
+import generators
 
 pytestmark = pytest.mark.gpu
 
@@ -232,7 +233,7 @@ def test_reference_contiguous_shape(g, expected, n, k, layout):
     e = g - 1
     s, mi = int(starts[e]), ms[e]
     dd = torch.empty((mi, n), dtype=torch.bfloat16, device=DEV)
-    deep_gemm.fp8_gemm_nt((a[0][s:s + mi], a[1][s:s + mi]), (bq[e], bs[e]), dd)
+    generators.dense_call_same_order(deep_gemm, (a[0][s:s + mi], a[1][s:s + mi]), (bq[e], bs[e]), dd)
     assert torch.equal(dd.view(torch.int16), d[s:s + mi].view(torch.int16)), f'expert {e} differs from a dense call'
     rerun_identical(call, d)
 
@@ -312,6 +313,6 @@ def test_reference_masked_shape(g, expected, n, k, psum):
     check(f'masked G={g} m={expected} {n}x{k} psum={psum}', np.concatenate(outs), np.concatenate(refs), k)
     e = g - 1
     dd = torch.empty((masked[e], n), dtype=torch.bfloat16, device=DEV)
-    deep_gemm.fp8_gemm_nt(a_rows[e], (bq[e], bs[e]), dd)
+    generators.dense_call_same_order(deep_gemm, a_rows[e], (bq[e], bs[e]), dd)
     assert torch.equal(dd.view(torch.int16), d_rows[e].view(torch.int16)), f'expert {e} differs from a dense call'
     rerun_identical(call, d)
