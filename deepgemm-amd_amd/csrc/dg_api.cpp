@@ -30,11 +30,15 @@ constexpr int kDefaultMKAlignment = 128;
 // (measured on MI355X over the DeepSeek-V3 (N, K) shapes: faster than every
 // tiled configuration up to 64 rows, slower from 128).
 constexpr int kDenseStreamRows = 64;
-// Dense calls of at most 16 rows take the tiny-M kernel (K split over a
+// Dense calls of at most 64 rows take the tiny-M kernel (K split over a
 // workgroup's waves, N / 16 or N / 32 workgroups) unless the streaming kernel
-// already has this many workgroups (N >= 8192 or so); measured on MI355X at
-// M = 1 and 16: 1.2-2.6x faster for N <= 7168, slower at N = 24576 and 32768.
+// already has this many workgroups (N >= 8192 or so), or the call has more than
+// 32 rows and fewer than 32 K blocks. Measured on MI355X at M = 1, 16, 17, 32
+// and 64: 1.2-2.6x faster for N <= 7168, slower at N = 24576 and 32768 and
+// even at 7168 x 2048 with 64 rows.
 constexpr int kTinyMStreamGrid = 64;
+
+bool tinym_preferred(int64_t m, int64_t k) { return m <= 32 || k / 128 >= 32; }
 
 // Tiny-M configuration (measured): 8 waves when the rows are few and each wave
 // gets at least 4 K blocks, else 4 (fewer workgroup-wide A re-reads per K
@@ -437,15 +441,16 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         // the rows that exist (16 x 16 x 128 MFMAs up to 16 rows).
         const bool stream_ok = fp8_masked_stream_supported(args) &&
                                (kind == kMasked || (kind == kNormal && m_rows <= kMaskedStreamRows));
-        // Dense calls of at most 16 rows: K split over the waves of a workgroup, so
-        // the launch has N / 16 workgroups instead of the streaming kernel's N / 128.
+        // Dense calls of at most 64 rows: K split over the waves of a workgroup, so
+        // the launch has N / 16 or N / 32 workgroups instead of the streaming
+        // kernel's N / 128.
         const bool tinym_ok = kind == kNormal && fp8_tinym_supported(args);
         if (tv == 8 || tv == 9) {   // forced: the tiny-M kernel
             if (!tinym_ok)
-                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 16 rows with "
+                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 64 rows with "
                                "K % 128 == 0, BF16 D and no C");
             t = {kTinyMRows, g_tile_n.load(), tv};
-        } else if (tv == 0 && tinym_ok &&
+        } else if (tv == 0 && tinym_ok && tinym_preferred(m_rows, k) &&
                    (!stream_ok || (n + 32 * fp8_masked_stream_waves(n, 1, args.grid_limit) - 1) /
                                           (32 * fp8_masked_stream_waves(n, 1, args.grid_limit)) <
                                       kTinyMStreamGrid)) {

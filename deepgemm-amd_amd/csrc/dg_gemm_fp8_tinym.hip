@@ -1,9 +1,9 @@
-// Dense FP32-scale FP8 GEMM for at most 16 rows of A (gfx950): decode-sized
+// Dense FP32-scale FP8 GEMM for at most 64 rows of A (gfx950): decode-sized
 // fp8_gemm_nt calls, D[m, n] = sum_k A[m, k] B[n, k] with the per-128-K FP32
 // promotion of the reference's 1D2D kernel
 // (deep_gemm/include/deep_gemm/impls/sm90_fp8_gemm_1d2d.cuh:281-345).
 //
-// At M <= 16 the call is a weight stream: N x K bytes of B against 16 x K of A.
+// At M <= 64 the call is a weight stream: N x K bytes of B against M x K of A.
 // The streaming kernel gives each workgroup 32 columns per wave and all of K,
 // so a launch has only N / 128 .. N / 256 workgroups (17 for N = 2112) and most
 // CUs stay idle. Here a workgroup owns 16 columns and splits K over its waves
@@ -13,8 +13,10 @@
 //    v_mfma_f32_16x16x128_f8f6f4 per block and column group (operand lane l:
 //    row l & 15, K bytes [32 (l >> 4), +32) of the block; result lane l: column
 //    4 (l >> 4) + e of token l & 15) and promotes it, fin = fma(sa * sb, acc,
-//    fin). Since the waves split K, every workgroup reads all of A (from L2):
-//    N / (16 CG) times A's bytes, which is why CG > 1 pays at large N;
+//    fin); with RT row tiles of 16 (M <= 16 RT), each K block also loads RT A
+//    fragments and issues RT x CG MFMAs. Since the waves split K, every
+//    workgroup reads all of A (from L2): N / (16 CG) times A's bytes, which is
+//    why CG > 1 pays at large N and M;
 //  * the fragments come straight from global memory into registers (a lane's
 //    32 bytes are contiguous in its row), kept PD blocks ahead in a register
 //    ring; no LDS, no barrier in the K loop;
@@ -25,7 +27,7 @@
 // grouped differently from the single-pass kernels (per wave, then across
 // waves), so the bits differ from theirs; it is its own configuration
 // (variant 8).
-// Requirements (checked by the host): M <= 16, K a multiple of 128, BF16 D
+// Requirements (checked by the host): M <= 64, K a multiple of 128, BF16 D
 // without C, 16-byte aligned A and B rows.
 #include <hip/hip_runtime.h>
 
@@ -38,20 +40,22 @@ namespace {
 using namespace dev;
 
 constexpr int kBK = 128;
-constexpr int kRows = 16;
-constexpr int kPD = 4;   // K blocks in flight per wave
+constexpr int kRows = 64;
 
-template <int CG>
+template <int RT, int CG>
 struct Frag {
-    i32x4 b0[CG], b1[CG], a0, a1;
-    float sa;
+    i32x4 b0[CG], b1[CG], a0[RT], a1[RT];
+    float sa[RT];
 };
 
-template <int NW, int CG>
+template <int NW, int RT, int CG>
 __global__ void __launch_bounds__(NW * 64)
 fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
     static_assert(CG == 1 || CG == 2 || CG == 4, "16, 32 or 64 columns");
-    __shared__ __attribute__((aligned(16))) float red[NW][CG][64][4];
+    static_assert(RT >= 1 && RT <= 4, "row tiles");
+    // K blocks in flight per wave (fewer with more fragments per block, for registers)
+    constexpr int kPD = RT * 2 + CG * 2 > 8 ? 2 : 4;
+    __shared__ __attribute__((aligned(16))) float red[NW][RT * CG][64][4];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * (16 * CG);
@@ -59,18 +63,23 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
     const int num_kb = p.k / kBK;
 
     // Rows past the edge read the last row that exists; their outputs are not stored.
-    const int m = min(r, p.m - 1);
     const uint8_t* __restrict__ b_row[CG];
 #pragma unroll
     for (int c = 0; c < CG; ++c) b_row[c] = p.b + (int64_t)min(n0 + 16 * c + r, p.n - 1) * p.ldb + 32 * q;
-    const uint8_t* __restrict__ a_row = p.a + (int64_t)m * p.lda + 32 * q;
-    const float* __restrict__ sa_row = p.sfa + (int64_t)m * p.sfa_sm;
+    const uint8_t* __restrict__ a_row[RT];
+    const float* __restrict__ sa_row[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int m = min(16 * t + r, p.m - 1);
+        a_row[t] = p.a + (int64_t)m * p.lda + 32 * q;
+        sa_row[t] = p.sfa + (int64_t)m * p.sfa_sm;
+    }
     // the workgroup's 16 CG columns lie in one 128-row SFB block
     const float* __restrict__ sb_col = p.sfb + (int64_t)(n0 >> 7) * p.sfb_sn;
 
     // this wave's blocks: kb = wave + NW * i, i < cnt
     const int cnt = wave < num_kb ? (num_kb - 1 - wave) / NW + 1 : 0;
-    auto load = [&](Frag<CG>& f, int i) {
+    auto load = [&](Frag<RT, CG>& f, int i) {
         const int kb = wave + NW * min(i, cnt - 1);   // past the end: the last block again
 #pragma unroll
         for (int c = 0; c < CG; ++c) {
@@ -78,17 +87,22 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
             f.b0[c] = *reinterpret_cast<const i32x4*>(bp);
             f.b1[c] = *reinterpret_cast<const i32x4*>(bp + 16);
         }
-        const uint8_t* ap = a_row + (int64_t)kb * kBK;
-        f.a0 = *reinterpret_cast<const i32x4*>(ap);
-        f.a1 = *reinterpret_cast<const i32x4*>(ap + 16);
-        f.sa = sa_row[(int64_t)kb * p.sfa_sk];
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint8_t* ap = a_row[t] + (int64_t)kb * kBK;
+            f.a0[t] = *reinterpret_cast<const i32x4*>(ap);
+            f.a1[t] = *reinterpret_cast<const i32x4*>(ap + 16);
+            f.sa[t] = sa_row[t][(int64_t)kb * p.sfa_sk];
+        }
     };
 
-    f32x4 fin[CG];
+    f32x4 fin[RT][CG];
 #pragma unroll
-    for (int c = 0; c < CG; ++c) fin[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int c = 0; c < CG; ++c) fin[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (cnt > 0) {
-        Frag<CG> ring[kPD];
+        Frag<RT, CG> ring[kPD];
 #pragma unroll
         for (int s = 0; s < kPD; ++s) load(ring[s], s);
         for (int i0 = 0; i0 < cnt; i0 += kPD) {
@@ -96,47 +110,57 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
             for (int s = 0; s < kPD; ++s) {
                 const int i = i0 + s;
                 if (i < cnt) {
-                    const Frag<CG> f = ring[s];
+                    const Frag<RT, CG> f = ring[s];
                     load(ring[s], i + kPD);
                     const float sb = sb_col[(int64_t)(wave + NW * i) * p.sfb_sk];
-                    const float s_ab = f.sa * sb;
-                    const i32x8 af = {f.a0[0], f.a0[1], f.a0[2], f.a0[3], f.a1[0], f.a1[1], f.a1[2], f.a1[3]};
 #pragma unroll
-                    for (int c = 0; c < CG; ++c) {
-                        const i32x8 bf = {f.b0[c][0], f.b0[c][1], f.b0[c][2], f.b0[c][3],
-                                          f.b1[c][0], f.b1[c][1], f.b1[c][2], f.b1[c][3]};
-                        const f32x4 acc =
-                            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af, f32x4{}, 0, 0, 0, 0, 0, 0);
+                    for (int t = 0; t < RT; ++t) {
+                        const float s_ab = f.sa[t] * sb;
+                        const i32x8 af = {f.a0[t][0], f.a0[t][1], f.a0[t][2], f.a0[t][3],
+                                          f.a1[t][0], f.a1[t][1], f.a1[t][2], f.a1[t][3]};
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) fin[c][e] = __builtin_fmaf(s_ab, acc[e], fin[c][e]);
+                        for (int c = 0; c < CG; ++c) {
+                            const i32x8 bf = {f.b0[c][0], f.b0[c][1], f.b0[c][2], f.b0[c][3],
+                                              f.b1[c][0], f.b1[c][1], f.b1[c][2], f.b1[c][3]};
+                            const f32x4 acc =
+                                __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af, f32x4{}, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) fin[t][c][e] = __builtin_fmaf(s_ab, acc[e], fin[t][c][e]);
+                        }
                     }
                 }
             }
         }
     }
 #pragma unroll
-    for (int c = 0; c < CG; ++c) *reinterpret_cast<f32x4*>(&red[wave][c][lane][0]) = fin[c];
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int c = 0; c < CG; ++c) *reinterpret_cast<f32x4*>(&red[wave][t * CG + c][lane][0]) = fin[t][c];
     __syncthreads();
-    // wave c < CG adds column group c's partial sums in wave order
-    if (wave >= CG) return;
-    const int c = wave;
-    f32x4 v = *reinterpret_cast<const f32x4*>(&red[0][c][lane][0]);
+    // output fragment fi (row tile fi / CG, column group fi % CG) is added up by
+    // wave fi % NW, in wave order
+    for (int fi = wave; fi < RT * CG; fi += NW) {
+        const int t = fi / CG, c = fi % CG;
+        f32x4 v = *reinterpret_cast<const f32x4*>(&red[0][fi][lane][0]);
 #pragma unroll
-    for (int w = 1; w < NW; ++w) {
-        const f32x4 u = *reinterpret_cast<const f32x4*>(&red[w][c][lane][0]);
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 u = *reinterpret_cast<const f32x4*>(&red[w][fi][lane][0]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v[e] + u[e];
-    }
-    // lane l: token l & 15, columns n0 + 16 c + 4 (l >> 4) + (0..3)
-    const int col = n0 + 16 * c + 4 * q;
-    if (r >= p.m || col >= p.n) return;
-    uint16_t* dp = static_cast<uint16_t*>(p.d) + (int64_t)r * p.ldd + col;
-    if (col + 4 <= p.n) {
-        *reinterpret_cast<uint2*>(dp) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    } else {
+            for (int e = 0; e < 4; ++e) v[e] = v[e] + u[e];
+        }
+        // lane l: token 16 t + (l & 15), columns n0 + 16 c + 4 (l >> 4) + (0..3)
+        const int row = 16 * t + r;
+        const int col = n0 + 16 * c + 4 * q;
+        if (row < p.m && col < p.n) {
+            uint16_t* dp = static_cast<uint16_t*>(p.d) + (int64_t)row * p.ldd + col;
+            if (col + 4 <= p.n) {
+                *reinterpret_cast<uint2*>(dp) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (col + e < p.n) dp[e] = bf16_bits(v[e]);
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < p.n) dp[e] = bf16_bits(v[e]);
+            }
+        }
     }
 }
 
@@ -147,23 +171,34 @@ bool fp8_tinym_supported(const Fp8GemmArgs& a) {
            a.num_groups == 1 && a.layout == nullptr;
 }
 
-template <int NW, int CG>
-void launch_nw_cg(const Fp8GemmArgs& a, hipStream_t stream) {
+template <int NW, int RT, int CG>
+void launch_cfg(const Fp8GemmArgs& a, hipStream_t stream) {
     const int64_t grid = (a.n + 16 * CG - 1) / (16 * CG);
     DG_CHECK(grid < (int64_t)1 << 31);
-    hipLaunchKernelGGL((fp8_gemm_tinym_kernel<NW, CG>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a);
+    hipLaunchKernelGGL((fp8_gemm_tinym_kernel<NW, RT, CG>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a);
+}
+
+template <int RT>
+void launch_rt(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream) {
+    switch (waves * 100 + cols) {
+        case 416: launch_cfg<4, RT, 1>(a, stream); break;
+        case 432: launch_cfg<4, RT, 2>(a, stream); break;
+        case 816: launch_cfg<8, RT, 1>(a, stream); break;
+        case 832: launch_cfg<8, RT, 2>(a, stream); break;
+        // (64 columns with more than 32 rows would not fit the registers)
+        case 464: if constexpr (RT <= 2) { launch_cfg<4, RT, 4>(a, stream); break; } else { [[fallthrough]]; }
+        case 864: if constexpr (RT <= 2) { launch_cfg<8, RT, 4>(a, stream); break; } else { [[fallthrough]]; }
+        default: DG_UNSUPPORTED("tiny-M kernel: 4 or 8 waves, 16, 32 or 64 columns per workgroup (64 up to 32 rows)");
+    }
 }
 
 void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream) {
     DG_CHECK(fp8_tinym_supported(a));
-    switch (waves * 100 + cols) {
-        case 416: launch_nw_cg<4, 1>(a, stream); break;
-        case 432: launch_nw_cg<4, 2>(a, stream); break;
-        case 464: launch_nw_cg<4, 4>(a, stream); break;
-        case 816: launch_nw_cg<8, 1>(a, stream); break;
-        case 832: launch_nw_cg<8, 2>(a, stream); break;
-        case 864: launch_nw_cg<8, 4>(a, stream); break;
-        default: DG_UNSUPPORTED("tiny-M kernel: 4 or 8 waves, 16, 32 or 64 columns per workgroup");
+    switch ((a.m + 15) / 16) {
+        case 1: launch_rt<1>(a, waves, cols, stream); break;
+        case 2: launch_rt<2>(a, waves, cols, stream); break;
+        case 3: launch_rt<3>(a, waves, cols, stream); break;
+        default: launch_rt<4>(a, waves, cols, stream); break;
     }
     DG_HIP_CHECK(hipGetLastError());
 }

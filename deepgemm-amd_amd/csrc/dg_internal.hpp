@@ -91,9 +91,9 @@ struct TileConfig {
     int variant = 1;
 };
 
-// Dense calls of at most 16 rows with K split over the waves of a workgroup
-// (dg_gemm_fp8_tinym.hip): M <= 16, K % 128 == 0, BF16 D, no C.
-constexpr int kTinyMRows = 16;
+// Dense calls of at most 64 rows with K split over the waves of a workgroup
+// (dg_gemm_fp8_tinym.hip): M <= 64, K % 128 == 0, BF16 D, no C.
+constexpr int kTinyMRows = 64;
 bool fp8_tinym_supported(const Fp8GemmArgs& a);
 void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream);
 
