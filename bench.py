@@ -16,7 +16,8 @@ Other workloads (`--workload`): dense_acc (FP32 C += A.B^T), contiguous
 (config 3, 8 experts, 32768 tokens), masked (config 4, 16 experts, max_m 256),
 fp8fp4 (config 5), cast (the fused per-token FP8 activation cast that produces
 A and its MN-major SFA for these GEMMs; HBM-bound, reported in GB/s), kgrouped
-(k_grouped_fp8_gemm_nt_contiguous, the 1D1D weight-gradient GEMM).
+(k_grouped_fp8_gemm_nt_contiguous, the 1D1D weight-gradient GEMM), decode
+(config 1's shape, 64 x 2112 x 7168, on the GPU).
 
 Prints one JSON line. `roofline` is computed from per-launch durations measured
 live with HIP events on the launch stream; `cpu_baseline` times the oracle/
@@ -41,7 +42,8 @@ DENSE_NK = [(2112, 7168), (24576, 1536), (7168, 16384), (4096, 7168), (7168, 204
 PROFILE_NAMES = {'dense': 'fp8_gemm_nt_dense_m4096', 'dense_acc': 'fp8_gemm_nt_dense_acc_m4096',
                  'contiguous': 'm_grouped_fp8_gemm_nt_contiguous_e8_t32768',
                  'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096',
-                 'cast': 'per_token_cast_to_fp8_bf16', 'kgrouped': 'k_grouped_fp8_gemm_nt_e8_m4096_n7168'}
+                 'cast': 'per_token_cast_to_fp8_bf16', 'kgrouped': 'k_grouped_fp8_gemm_nt_e8_m4096_n7168',
+                 'decode': 'fp8_gemm_nt_m64_n2112_k7168'}
 
 
 def parse():
@@ -50,7 +52,7 @@ def parse():
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--workload', default='dense',
-                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped'])
+                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped', 'decode'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-extras', action='store_true',
                     help='default workload only: skip the per-launch summaries of the other configurations')
@@ -226,6 +228,25 @@ def make_dense(acc: bool):
     return launches, cfg
 
 
+def make_decode():
+    """Config 1's shape on the GPU: dense fp8_gemm_nt, A [64, 7168] (1x128 FP32
+    scales), B [2112, 7168] (128x128 FP32 scales), BF16 D: a decode-sized call
+    (the configuration the CPU baseline of the reference is quoted on)."""
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    gen = torch.Generator().manual_seed(1)
+    m, n, k = 64, 2112, 7168
+    a, b = _quant_a(m, k, gen, dev), _quant_b(n, k, gen, dev)
+
+    def mk():
+        a2, b2 = _twin(a), _twin(b)
+        d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2)
+    cfg = {'workload': 'fp8_gemm_nt M=64 N=2112 K=7168 (config 1 shape)', 'm': m, 'n': n, 'k': k, 'out': 'bf16'}
+    return [Launch('m64_n2112_k7168', mk, 2 * m * n * k, _dense_bytes(m, n, k, 2 * m * n))], cfg
+
+
 def make_contiguous():
     import torch
     import deep_gemm
@@ -395,6 +416,8 @@ def cpu_baseline(workload: str, sample_m: int):
                      'sample': f'M={rows} rows of each (M,K) shape: the oracle\'s numpy per-token cast '
                                f'(single-threaded numpy), {secs:.2f} s per pass (median)'}, **host)
     nk = DENSE_NK if workload in ('dense', 'dense_acc') else [(4096, 7168), (7168, 2048)]
+    if workload == 'decode':   # config 1 itself: the whole 64-row workload
+        nk, sample_m = [(2112, 7168)], 64
     flops, secs = 0, 0.0
     for n, k in nk:
         a = torch.randn((sample_m, k), generator=torch.Generator().manual_seed(1)).bfloat16().float().numpy()
@@ -431,10 +454,10 @@ def load_traffic(workload, launches, configs):
 
 MAKERS = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
           'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast,
-          'kgrouped': make_kgrouped}
+          'kgrouped': make_kgrouped, 'decode': make_decode}
 # Configurations summarized next to the headline in the default run (per-launch
 # kernel time and roofline fraction; the headline `value` stays config 2).
-EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4']
+EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4', 'decode']
 
 
 def t_min_us(flops, nbytes):
