@@ -30,7 +30,8 @@ import json
 import os
 import sys
 
-GEMM_KEYS = ('fp8_gemm_1d2d', 'fp8_fp4_gemm', 'fp8_gemm_1d2d_pipe', 'fp8_gemm_masked_stream', 'fp8_gemm_1d1d')
+GEMM_KEYS = ('fp8_gemm_1d2d', 'fp8_fp4_gemm', 'fp8_gemm_1d2d_pipe', 'fp8_gemm_masked_stream', 'fp8_gemm_1d1d',
+             'fp8_gemm_tinym')
 CAST_KEYS = ('per_token_cast_kernel',)   # the cast workload's kernel (GEMM workloads also cast while setting up)
 COPY_KEY = 'neg_kernel'
 _KEYS = GEMM_KEYS
