@@ -15,6 +15,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "dg_kernel_common.hpp"
 #include "dg_lds_dma.hpp"
 
@@ -77,6 +79,41 @@ struct RowEpilogue {
             smask[h] = __ballot(st);
             zmask[h] = __ballot(z);
         }
+        // ---- C, loaded ahead of the stores: a load placed after a store would
+        // wait for it (C may be D itself, so the compiler keeps them in order),
+        // one memory round trip per row segment. So each pass loads all of its C
+        // once its accumulators are staged, before its stores. (Loading the next
+        // pass's C there too spills registers.) Every element is still read
+        // before it is written. Only whole VPL-wide
+        // segments of stored rows are prefetched, and nothing else is written to
+        // cpre (a merged default value would make the compiler copy, and so wait
+        // for, each load right away); the rare partial segment at the right edge
+        // loads its C in the loop.
+        constexpr int NIT = (RPP + RPI - 1) / RPI;
+        constexpr int NPASS = WM / RPP;
+        using CVec = std::conditional_t<OUT_F32, f32x4, uint4>;
+        CVec cpre[HAS_C ? NPASS : 1][HAS_C ? NIT : 1];
+        auto prefetch_c = [&](int pp) {
+            if constexpr (HAS_C) {
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) {
+                    const int r = it * RPI + lane / LPR;
+                    const int m = row0 + pp * RPP + r;
+                    const int n = col0 + (lane % LPR) * VPL;
+                    const int wr = pp * RPP + r;
+                    constexpr bool POW2 = (NMASK & (NMASK - 1)) == 0;
+                    const int mi = POW2 ? ((wr >> 6) & (NMASK - 1)) : (wr >> 6);
+                    const uint64_t sm = NMASK == 1 ? smask[0] : smask[mi];
+                    const bool in = EXACT || (lane < RPI * LPR && r < RPP);
+                    if (in && ((sm >> (wr & 63)) & 1) && n + VPL <= n_total) {
+                        if constexpr (OUT_F32)
+                            cpre[pp][it] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(c) + (int64_t)m * ldc + n);
+                        else
+                            cpre[pp][it] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(c) + (int64_t)m * ldc + n);
+                    }
+                }
+            }
+        };
 #pragma unroll
         for (int p0 = 0; p0 < WM; p0 += RPP) {
             // ---- registers -> LDS (rows p0 .. p0 + RPP of the wave tile)
@@ -99,11 +136,12 @@ struct RowEpilogue {
                         }
                     }
             }
+            if constexpr (HAS_C) prefetch_c(p0 / RPP);
             // ---- LDS -> global, one row segment of VPL outputs per lane
             // (LDS operations of one wave complete in order, so the reads see the
             // writes above and the next pass's writes follow these reads.)
 #pragma unroll
-            for (int it = 0; it < (RPP + RPI - 1) / RPI; ++it) {
+            for (int it = 0; it < NIT; ++it) {
                 const int r = it * RPI + lane / LPR;
                 if (!EXACT && (lane >= RPI * LPR || r >= RPP)) continue;
                 const int v0 = (lane % LPR) * VPL;             // first column (wave-local)
@@ -151,13 +189,13 @@ struct RowEpilogue {
                 const bool full = n + VPL <= n_total;
                 if constexpr (OUT_F32) {
                     float* dp = static_cast<float*>(d) + d_goff + (int64_t)m * ldd + n;
-                    if (HAS_C && store) {
-                        const float* cp = static_cast<const float*>(c) + (int64_t)m * ldc + n;
-                        if (full) {
-                            const f32x4 cv = *reinterpret_cast<const f32x4*>(cp);
+                    if constexpr (HAS_C) {
+                        if (store && full) {
+                            const f32x4 cv = cpre[p0 / RPP][it];
 #pragma unroll
                             for (int e = 0; e < 4; ++e) v[e] = cv[e] + v[e];
-                        } else {
+                        } else if (store) {
+                            const float* cp = static_cast<const float*>(c) + (int64_t)m * ldc + n;
 #pragma unroll
                             for (int e = 0; e < 4; ++e)
                                 if (n + e < n_total) v[e] = cp[e] + v[e];
@@ -172,17 +210,17 @@ struct RowEpilogue {
                     }
                 } else {
                     uint16_t* dp = static_cast<uint16_t*>(d) + d_goff + (int64_t)m * ldd + n;
-                    if (HAS_C && store) {
-                        const uint16_t* cp = static_cast<const uint16_t*>(c) + (int64_t)m * ldc + n;
-                        if (full) {
-                            const uint4 cv = *reinterpret_cast<const uint4*>(cp);
+                    if constexpr (HAS_C) {
+                        if (store && full) {
+                            const uint4 cv = cpre[p0 / RPP][it];
                             const uint32_t w[4] = {cv.x, cv.y, cv.z, cv.w};
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 v[2 * e] = bf16_to_f32(static_cast<uint16_t>(w[e] & 0xffffu)) + v[2 * e];
                                 v[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(w[e] >> 16)) + v[2 * e + 1];
                             }
-                        } else {
+                        } else if (store) {
+                            const uint16_t* cp = static_cast<const uint16_t*>(c) + (int64_t)m * ldc + n;
 #pragma unroll
                             for (int e = 0; e < 8; ++e)
                                 if (n + e < n_total) v[e] = bf16_to_f32(cp[e]) + v[e];
