@@ -38,13 +38,12 @@ constexpr int kDenseStreamRows = 64;
 // even at 7168 x 2048 with 64 rows.
 constexpr int kTinyMStreamGrid = 64;
 
-bool tinym_preferred(int64_t m, int64_t k) { return m <= 32 || k / 128 >= 32; }
-
-// Tiny-M configuration (measured): 8 waves when the rows are few and each wave
-// gets at least 4 K blocks, else 4 (fewer workgroup-wide A re-reads per K
-// block); 32 columns per workgroup once N / 16 exceeds the CU count, else 16.
+// Tiny-M configuration (measured): 8 waves when the rows are few, K is long
+// (each wave gets at least 6 K blocks) and the workgroups are narrow, else 4
+// (fewer workgroup-wide A re-reads per K block); 32 columns per workgroup once
+// N / 16 exceeds the CU count, else 16.
 TileConfig choose_tinym(int64_t m, int64_t n, int64_t k) {
-    const int waves_variant = (m <= 4 && k / 128 >= 32) ? 8 : 9;
+    const int waves_variant = (m <= 16 && k / 128 >= 48 && n <= 4096) ? 8 : 9;
     const int cols = n > 4096 ? 32 : 16;
     return TileConfig{kTinyMRows, cols, waves_variant};
 }
@@ -448,9 +447,9 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         if (tv == 8 || tv == 9) {   // forced: the tiny-M kernel
             if (!tinym_ok)
                 DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 64 rows with "
-                               "K % 128 == 0, BF16 D and no C");
+                               "K % 128 == 0, K <= 32768, BF16 D and no C");
             t = {kTinyMRows, g_tile_n.load(), tv};
-        } else if (tv == 0 && tinym_ok && tinym_preferred(m_rows, k) &&
+        } else if (tv == 0 && tinym_ok &&
                    (!stream_ok || (n + 32 * fp8_masked_stream_waves(n, 1, args.grid_limit) - 1) /
                                           (32 * fp8_masked_stream_waves(n, 1, args.grid_limit)) <
                                       kTinyMStreamGrid)) {

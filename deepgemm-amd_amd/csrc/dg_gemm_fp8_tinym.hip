@@ -18,8 +18,9 @@
 //    workgroup reads all of A (from L2): N / (16 CG) times A's bytes, which is
 //    why CG > 1 pays at large N and M;
 //  * the fragments come straight from global memory into registers (a lane's
-//    32 bytes are contiguous in its row), kept PD blocks ahead in a register
-//    ring; no LDS, no barrier in the K loop;
+//    32 bytes are contiguous in its row), kept 2 to 8 blocks ahead in a
+//    register ring; no LDS, no barrier in the K loop; the B scales of a wave's
+//    blocks are loaded once, one per lane;
 //  * the NW partial sums meet in LDS and wave 0 adds them in wave order, so the
 //    result is deterministic (no atomics, no workspace); then one rounding to
 //    BF16.
@@ -27,8 +28,8 @@
 // grouped differently from the single-pass kernels (per wave, then across
 // waves), so the bits differ from theirs; it is its own configuration
 // (variant 8).
-// Requirements (checked by the host): M <= 64, K a multiple of 128, BF16 D
-// without C, 16-byte aligned A and B rows.
+// Requirements (checked by the host): M <= 64, K a multiple of 128 and at most
+// 32768, BF16 D without C, 16-byte aligned A and B rows.
 #include <hip/hip_runtime.h>
 
 #include "dg_internal.hpp"
@@ -41,6 +42,7 @@ using namespace dev;
 
 constexpr int kBK = 128;
 constexpr int kRows = 64;
+constexpr int kMaxKBlocks = 64 * 4;   // a wave's B scales fit one register: 64 blocks of 4 waves
 
 template <int RT, int CG>
 struct Frag {
@@ -48,13 +50,20 @@ struct Frag {
     float sa[RT];
 };
 
+// K blocks in flight per wave: as many as fit in about 136 registers (2 to 8),
+// so that a wave stays within 256 registers
+template <int RT, int CG>
+constexpr int ring_depth() {
+    constexpr int d = 136 / (8 * CG + 9 * RT);
+    return d < 2 ? 2 : d > 8 ? 8 : d;
+}
+
 template <int NW, int RT, int CG>
 __global__ void __launch_bounds__(NW * 64)
 fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
     static_assert(CG == 1 || CG == 2 || CG == 4, "16, 32 or 64 columns");
     static_assert(RT >= 1 && RT <= 4, "row tiles");
-    // K blocks in flight per wave (fewer with more fragments per block, for registers)
-    constexpr int kPD = RT * 2 + CG * 2 > 8 ? 2 : 4;
+    constexpr int kPD = ring_depth<RT, CG>();
     __shared__ __attribute__((aligned(16))) float red[NW][RT * CG][64][4];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -74,11 +83,14 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
         a_row[t] = p.a + (int64_t)m * p.lda + 32 * q;
         sa_row[t] = p.sfa + (int64_t)m * p.sfa_sm;
     }
-    // the workgroup's 16 CG columns lie in one 128-row SFB block
-    const float* __restrict__ sb_col = p.sfb + (int64_t)(n0 >> 7) * p.sfb_sn;
 
-    // this wave's blocks: kb = wave + NW * i, i < cnt
+    // this wave's blocks: kb = wave + NW * i, i < cnt (cnt <= 64: the host bounds K)
     const int cnt = wave < num_kb ? (num_kb - 1 - wave) / NW + 1 : 0;
+    // the workgroup's 16 CG columns lie in one 128-row SFB block; lane j holds
+    // the B scale of block wave + NW j
+    const float* __restrict__ sb_col = p.sfb + (int64_t)(n0 >> 7) * p.sfb_sn;
+    const float sbv = lane < cnt ? sb_col[(int64_t)(wave + NW * lane) * p.sfb_sk] : 0.f;
+
     auto load = [&](Frag<RT, CG>& f, int i) {
         const int kb = wave + NW * min(i, cnt - 1);   // past the end: the last block again
 #pragma unroll
@@ -102,35 +114,60 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
 #pragma unroll
         for (int c = 0; c < CG; ++c) fin[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (cnt > 0) {
+        // Each slot is multiplied in place and then refilled, so no loaded register
+        // is ever copied (a copy would wait for its load) and the compiler's wait
+        // before a slot's first use covers exactly the loads issued before it. The
+        // blocks are walked in whole rings; slots past the wave's last block hold
+        // that block again and are added with scale 0.
         Frag<RT, CG> ring[kPD];
+        // (slot by slot, in the order the loop refills them: the compiler's wait
+        // counts inside the loop hold for the loads issued here as well)
 #pragma unroll
-        for (int s = 0; s < kPD; ++s) load(ring[s], s);
-        for (int i0 = 0; i0 < cnt; i0 += kPD) {
+        for (int s = 0; s < kPD; ++s) {
+            load(ring[s], s);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // slot s of ring `it` holds block it * kPD + s; the last ring issues no refills
+        auto step = [&](Frag<RT, CG>& f, int i, bool refill) {
+            // (read unconditionally and then selected: a branch around the read
+            // would split the loop body into blocks the scheduler cannot order)
+            const float sb_i = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sbv), min(i, 63)));
+            const float sb = i < cnt ? sb_i : 0.f;
+            float s_ab[RT];
+            f32x4 acc[RT][CG];
 #pragma unroll
-            for (int s = 0; s < kPD; ++s) {
-                const int i = i0 + s;
-                if (i < cnt) {
-                    const Frag<RT, CG> f = ring[s];
-                    load(ring[s], i + kPD);
-                    const float sb = sb_col[(int64_t)(wave + NW * i) * p.sfb_sk];
+            for (int t = 0; t < RT; ++t) {
+                s_ab[t] = f.sa[t] * sb;
+                const i32x8 af = {f.a0[t][0], f.a0[t][1], f.a0[t][2], f.a0[t][3],
+                                  f.a1[t][0], f.a1[t][1], f.a1[t][2], f.a1[t][3]};
 #pragma unroll
-                    for (int t = 0; t < RT; ++t) {
-                        const float s_ab = f.sa[t] * sb;
-                        const i32x8 af = {f.a0[t][0], f.a0[t][1], f.a0[t][2], f.a0[t][3],
-                                          f.a1[t][0], f.a1[t][1], f.a1[t][2], f.a1[t][3]};
-#pragma unroll
-                        for (int c = 0; c < CG; ++c) {
-                            const i32x8 bf = {f.b0[c][0], f.b0[c][1], f.b0[c][2], f.b0[c][3],
-                                              f.b1[c][0], f.b1[c][1], f.b1[c][2], f.b1[c][3]};
-                            const f32x4 acc =
-                                __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af, f32x4{}, 0, 0, 0, 0, 0, 0);
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) fin[t][c][e] = __builtin_fmaf(s_ab, acc[e], fin[t][c][e]);
-                        }
-                    }
+                for (int c = 0; c < CG; ++c) {
+                    const i32x8 bf = {f.b0[c][0], f.b0[c][1], f.b0[c][2], f.b0[c][3],
+                                      f.b1[c][0], f.b1[c][1], f.b1[c][2], f.b1[c][3]};
+                    acc[t][c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf, af, f32x4{}, 0, 0, 0, 0, 0, 0);
                 }
             }
+            if (refill) {
+                // the slot's registers are read (MFMA operands, scale product)
+                // before the refill is issued into them; the promotion waits for
+                // the MFMAs after it
+                __builtin_amdgcn_sched_barrier(0);
+                load(f, i + kPD);
+            }
+#pragma unroll
+            for (int t = 0; t < RT; ++t)
+#pragma unroll
+                for (int c = 0; c < CG; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) fin[t][c][e] = __builtin_fmaf(s_ab[t], acc[t][c][e], fin[t][c][e]);
+        };
+        const int rings = (cnt + kPD - 1) / kPD;
+        for (int it = 0; it + 1 < rings; ++it) {
+#pragma unroll
+            for (int s = 0; s < kPD; ++s) step(ring[s], it * kPD + s, true);
         }
+#pragma unroll
+        for (int s = 0; s < kPD; ++s) step(ring[s], (rings - 1) * kPD + s, false);
     }
 #pragma unroll
     for (int t = 0; t < RT; ++t)
@@ -167,7 +204,8 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
 }  // namespace
 
 bool fp8_tinym_supported(const Fp8GemmArgs& a) {
-    return a.m > 0 && a.m <= kRows && a.n > 0 && a.k > 0 && a.k % kBK == 0 && !a.out_f32 && a.c == nullptr &&
+    return a.m > 0 && a.m <= kRows && a.n > 0 && a.k > 0 && a.k % kBK == 0 && a.k / kBK <= kMaxKBlocks &&
+           !a.out_f32 && a.c == nullptr &&
            a.num_groups == 1 && a.layout == nullptr;
 }
 

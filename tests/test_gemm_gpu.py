@@ -457,16 +457,16 @@ def test_dense_tiny_m_on_stream_kernel(m):
 
 @pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (5, 2112, 7168), (16, 7168, 2048), (3, 104, 384),
                                    (16, 24576, 1536), (7, 4096, 16384), (1, 576, 128), (33, 2112, 7168),
-                                   (64, 2112, 7168), (50, 104, 1024), (17, 4096, 4096)])
+                                   (64, 2112, 7168), (50, 104, 1024), (17, 4096, 4096), (3, 104, 32768)])
 def test_dense_tiny_m_split_k_kernel(m, n, k):
     """The tiny-M kernel (K split over the waves of a workgroup, partial sums
     added in wave order; up to four 16-row tiles), in each of its configurations
     (8 or 4 waves; 16, 32 or 64 columns per workgroup, 64 up to 32 rows): the
     oracle within one BF16 ulp plus the FP32 accumulation bound, ragged M and N
     (104, not a multiple of 16 or 32), fewer K blocks than waves (K = 128, 384),
-    MN-major SFA equal to K-major, and bitwise-identical reruns. The default
-    routing takes it for N up to 7168 (above 32 rows only with >= 32 K blocks);
-    config 1 of the benchmark (64 x 2112 x 7168) is one of these."""
+    the largest K (256 blocks: 64 per wave at 4 waves), MN-major SFA equal to
+    K-major, and bitwise-identical reruns. The default routing takes it for N
+    up to 7168; config 1 of the benchmark (64 x 2112 x 7168) is one of these."""
     x = gen.dense_inputs(m, n, k, seed=90 + m + n)
     ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
@@ -490,7 +490,7 @@ def test_dense_tiny_m_split_k_kernel(m, n, k):
         print(f'  {cfg}', flush=True)
         if v:
             assert f' v{v} ' in cfg and f'block_n={bn} ' in cfg, cfg
-        elif n <= 7168 and (m <= 32 or k >= 32 * 128):
+        elif n <= 7168:
             assert ' v8 ' in cfg or ' v9 ' in cfg, cfg
         out = d.float().cpu().numpy()
         diff, _ = report(f'dense tiny M={m} N={n} K={k} [{cfg.split(" kind")[0]} {bn}]', out, ref)
@@ -499,18 +499,43 @@ def test_dense_tiny_m_split_k_kernel(m, n, k):
         assert torch.equal(d2.view(torch.int16), d.view(torch.int16))
 
 
+def test_dense_tiny_m_k_bound():
+    """The tiny-M kernel keeps a wave's B scales in one register (at most 64 K
+    blocks per wave, 256 in all): with 257 K blocks a forced call is refused
+    before any launch, and the default routing takes a tiled kernel, which
+    agrees with the oracle."""
+    m, n, k = 3, 104, 257 * 128
+    x = gen.dense_inputs(m, n, k, seed=97)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    d = sentinel_bf16((m, n))
+    deep_gemm.set_tile_override(64, 16, variant=9)
+    try:
+        with pytest.raises(RuntimeError, match='tiny-M'):
+            deep_gemm.fp8_gemm_nt(a, b, d)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    torch.cuda.synchronize()
+    assert bool((d.view(torch.int16) == SENTINEL).all())
+    deep_gemm.fp8_gemm_nt(a, b, d)
+    cfg = deep_gemm.get_last_config()
+    assert ' v8 ' not in cfg and ' v9 ' not in cfg, cfg
+    out = d.float().cpu().numpy()
+    diff, _ = report(f'dense M={m} K={k} [{cfg.split(" kind")[0]}]', out, ref)
+    assert diff < 1e-3
+
+
 @pytest.mark.parametrize('m', [17, 33, 64])
 def test_dense_small_m_stream_equals_tiled(m):
-    """Dense calls of 17 to 64 rows on the weight-streaming kernel's 32 x 32 x 64
-    passes (block_m 160; the default for 33 to 64 rows at this K, forced
-    otherwise) are bitwise equal to the pipelined tiles (same MFMA pair, same
-    per-K-block promotion order) and to the oracle within one BF16 ulp."""
+    """Dense calls of 17 to 64 rows forced onto the weight-streaming kernel's
+    32 x 32 x 64 passes (block_m 160) are bitwise equal to the pipelined tiles
+    (same MFMA pair, same per-K-block promotion order) and to the oracle within
+    one BF16 ulp."""
     n, k = 7168, 2048
     x = gen.dense_inputs(m, n, k, seed=80 + m)
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
     d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
-    if m <= 32:
-        deep_gemm.set_tile_override(160, 224, variant=5)
+    deep_gemm.set_tile_override(160, 224, variant=5)
     try:
         deep_gemm.fp8_gemm_nt(a, b, d)
         cfg = deep_gemm.get_last_config()
