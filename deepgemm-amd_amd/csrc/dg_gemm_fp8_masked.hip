@@ -20,13 +20,18 @@
 //    after the expert's first workgroup). A(kb + S_A - 1) and B(kb + 2) are
 //    issued before K block kb computes, so two B stages are in flight while a
 //    block computes; B(0) and B(1) are issued before masked_m is even read;
-//  * a block's stage loads are spread over its row-tile iterations (A after
-//    the first MFMA pair, then one B load per iteration) rather than issued in
-//    one burst that would hold every wave at the load queue with the matrix
-//    core idle; B(kb + 2) has two blocks to land, A(kb + 1) all of block kb;
+//  * the 32-row passes run with four loader waves next to the NW compute waves:
+//    the loaders issue every stage load and wait for them, the compute waves
+//    issue no vector-memory instruction in the K loop (a full load queue holds
+//    a loader, never a wave with MFMAs to issue), and both meet at one barrier
+//    per K block. Three waves per SIMD leave 168 registers, so the compute
+//    waves keep one A fragment and one accumulator. The 16-row pass (and the
+//    NL = 0 instantiation) spreads each wave's share of the stage loads over
+//    its row tiles instead. B(kb + 2) has two blocks to land, A(kb + 1) one or
+//    two;
 //  * SFB comes in by scalar loads one K block ahead (no vector-memory count);
 //  * all stage loads are global_load_lds_dwordx4 / _dword with the same
-//    per-wave count, so one s_waitcnt vmcnt immediate serves every wave;
+//    count in every issuing wave, so one s_waitcnt vmcnt immediate serves them;
 //  * workgroups of one expert run on one XCD (logical tiles are expert-major
 //    and mapped to XCDs in contiguous ranges), so A rows reach HBM once per XCD.
 // A pass of at most 16 rows (small decode groups, and dense calls of at most 16
@@ -69,75 +74,162 @@ struct StreamShape {
     static constexpr int BN = NW * 32;
     static constexpr int B_STAGE = BN * kBK;
     static constexpr int B_RING = 3 * B_STAGE;
-    static constexpr int LB = BN / (8 * NW);   // B loads per stage and wave (= 4)
+    static constexpr int B_SEGS = BN / 8;      // 1 KB (8-column) wave loads per stage
+    static constexpr int LB = B_SEGS / NW;     // B loads per stage and wave when every wave loads (= 4)
 
-    // Column (LDS row) 8 * (i * NW + wave) + rs of load i, clamped to the last
-    // column that exists; the 16-byte chunk is swizzled by the LDS row.
-    __device__ static void offsets(uint32_t (&voff)[LB], int wave, int rs, int pc, int b_rows, int64_t ldb) {
+    // Load i of issuing wave `idx` (of STRIDE issuing waves) is entry i * STRIDE + idx:
+    // columns (LDS rows) 8 e + rs, clamped to the last column that exists; the
+    // 16-byte chunk is swizzled by the LDS row.
+    template <int L, int STRIDE>
+    __device__ static void offsets(uint32_t (&voff)[L], int idx, int rs, int pc, int b_rows, int64_t ldb) {
+        static_assert(L * STRIDE == B_SEGS, "every entry once");
 #pragma unroll
-        for (int i = 0; i < LB; ++i) {
-            const int row = (i * NW + wave) * 8 + rs;
+        for (int i = 0; i < L; ++i) {
+            const int row = (i * STRIDE + idx) * 8 + rs;
             voff[i] = (uint32_t)min(row, b_rows - 1) * (uint32_t)ldb + ((pc ^ swz_g(row)) << 4);
         }
     }
-    __device__ static void issue_one(const uint8_t* b_t, const uint32_t (&voff)[LB], int num_kb, int kb, int st,
-                                     int wave, uint32_t smem_lds, int i) {
+    template <int L, int STRIDE>
+    __device__ static void issue_one(const uint8_t* b_t, const uint32_t (&voff)[L], int num_kb, int kb, int st,
+                                     int idx, uint32_t smem_lds, int i) {
         kb = min(kb, num_kb - 1);
         const uint8_t* base = b_t + (int64_t)kb * kBK;
-        const uint32_t lds = smem_lds + st * B_STAGE + (i * NW + wave) * 1024;
+        const uint32_t lds = smem_lds + st * B_STAGE + (i * STRIDE + idx) * 1024;
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds), "v"(voff[i]),
                      "s"(base)
                      : "memory", "m0");
     }
-    __device__ static void issue(const uint8_t* b_t, const uint32_t (&voff)[LB], int num_kb, int kb, int st,
-                                 int wave, uint32_t smem_lds) {
-        kb = min(kb, num_kb - 1);   // past the end: reload the last block into the free slot
-        const uint8_t* base = b_t + (int64_t)kb * kBK;
+    template <int L, int STRIDE>
+    __device__ static void issue(const uint8_t* b_t, const uint32_t (&voff)[L], int num_kb, int kb, int st, int idx,
+                                 uint32_t smem_lds) {
+        // past the end: reload the last block into the free slot
 #pragma unroll
-        for (int i = 0; i < LB; ++i) {
-            const uint32_t lds = smem_lds + st * B_STAGE + (i * NW + wave) * 1024;
-            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds), "v"(voff[i]),
-                         "s"(base)
-                         : "memory", "m0");
-        }
+        for (int i = 0; i < L; ++i) issue_one<L, STRIDE>(b_t, voff, num_kb, kb, st, idx, smem_lds, i);
     }
+};
+
+// Loader waves of the 32-row passes (0: every wave loads and computes).
+constexpr int kMaskedLoaders = 4;
+
+// B load list of a pass: BL loads per stage and issuing wave, entry stride BS.
+template <int NW, int NL>
+struct BList {
+    static constexpr int BS = NL ? NL : NW;
+    static constexpr int BL = StreamShape<NW>::B_SEGS / BS;
 };
 
 // One pass over rows [r0, r0 + 32 * NRT) of the expert (a_rows of them valid).
 // b_primed: B(0) and B(1) are already in flight (issued by the caller).
-template <int NW, int NRT>
+// NL = 0: every wave issues its share of the stage loads between its MFMAs.
+// NL > 0: waves NW .. NW + NL - 1 are loaders: they issue every stage load and
+// wait for them, and the NW compute waves issue no vector-memory instruction
+// in the K loop, so a load queue that is full never holds a wave that has
+// MFMAs to issue. Both roles meet at one barrier per K block.
+template <int NW, int NRT, int NL>
 __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem, const uint8_t* b_t,
-                                            const uint32_t (&voff_b)[StreamShape<NW>::LB], bool b_primed, int g,
+                                            const uint32_t (&voff_b)[BList<NW, NL>::BL], bool b_primed, int g,
                                             int n0, int r0, int a_rows, int m_g, int wave, int lane) {
     using S = StreamShape<NW>;
+    using BLS = BList<NW, NL>;
     constexpr int ROWS = NRT * 32;
     constexpr int A_SEGS = ROWS / 8;                        // 1 KB (8-row) wave loads of A per stage
     constexpr int SA_SEGS = (ROWS + 63) / 64;               // 256 B (64-row) SFA loads per stage
     // A stage loads, one list: the A segments, then the SFA segments; load i of
-    // wave w is entry i * NW + w (past the end: the last entry again), so every
-    // wave issues LA loads and none repeats another's unless the list runs short.
+    // issuing wave w is entry i * AS + w (past the end: the last entry again), so
+    // every issuing wave issues LA loads and none repeats another's unless the
+    // list runs short.
     constexpr int A_LOADS = A_SEGS + SA_SEGS;
-    constexpr int LA = (A_LOADS + NW - 1) / NW;
+    constexpr int AS = NL ? NL : NW;
+    constexpr int LA = (A_LOADS + AS - 1) / AS;
     constexpr int A_STAGE = ROWS * kBK + SA_SEGS * 256;
     // A ring depth: as many stages as fit, at most 4, except with 8 waves
-    // (256-column tiles), where 2 measured faster than 3 (4096 x 7168: 113 against
-    // 117 us; fewer A loads in flight leave the load path to the B stream), while
-    // with 7 waves (7168 x 2048) 3 stay 1.5% faster than 2.
+    // (256-column tiles) that also load, where 2 measured faster than 3
+    // (4096 x 7168: 113 against 117 us; fewer A loads in flight leave the load
+    // path to the B stream), while with 7 waves (7168 x 2048) 3 stay 1.5% faster
+    // than 2.
     constexpr int SA_FIT = (kLds - S::B_RING) / A_STAGE > 4 ? 4 : (kLds - S::B_RING) / A_STAGE;
-    constexpr int SA = NW == 8 ? (SA_FIT < 2 ? SA_FIT : 2) : SA_FIT;
-    constexpr int LB = S::LB;
+    constexpr int SA = NW == 8 && NL == 0 ? (SA_FIT < 2 ? SA_FIT : 2) : SA_FIT;
+    constexpr int LB = BLS::BL;
     // At the end of block kb, A(kb + 1) and B(kb + 1) must be complete; the loads
-    // issued after the later of them are B(kb + 2) (two A stages) or all of
-    // block kb's (more).
+    // an issuing wave issued after the later of them are B(kb + 2) (two A stages)
+    // or all of block kb's (more).
     constexpr int W = SA == 2 ? LB : LA + LB;
     static_assert(SA >= 2, "two A stages fit");
-    static_assert(LA + LB < 64, "vmcnt range");
+    static_assert(LA + LB < 64 && (SA - 1) * LA + 2 * LB < 64, "vmcnt range");
+    // (lane and wave pass through an empty asm, so the compiler cannot hoist this
+    // pass's per-lane offsets above the kernel's switch over the passes, where
+    // every pass's offsets would be live at once)
+    asm volatile("" : "+v"(lane), "+s"(wave));
+    // issuing wave index and roles (wave-uniform)
+    const bool loader = NL > 0 && wave >= NW;
+    const int iw = NL ? max(wave - NW, 0) : wave;
 
     const int num_kb = p.k / kBK;
     const int lrow = lane & 31, lhalf = lane >> 5;
     const int rs = lane >> 3, pc = lane & 7;
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
     const uint32_t a_ring = smem_lds + S::B_RING;
+
+    const uint8_t* __restrict__ a_p = p.a + (int64_t)g * p.a_gs + (int64_t)r0 * p.lda;
+    const float* __restrict__ sa_p = p.sfa + (int64_t)g * p.sfa_gs + (int64_t)r0 * p.sfa_sm;
+
+    // Per-lane offsets of the wave's A stage loads (entry e = i * AS + iw of the
+    // list): rows past a_rows repeat the last valid one, whose outputs are never
+    // stored.
+    uint32_t voff_a[LA];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int e = min(i * AS + iw, A_LOADS - 1);
+        if (e < A_SEGS) {
+            const int row = e * 8 + rs;
+            voff_a[i] = (uint32_t)min(row, a_rows - 1) * (uint32_t)p.lda + ((pc ^ swz_g(row)) << 4);
+        } else {
+            voff_a[i] = (uint32_t)(min((e - A_SEGS) * 64 + lane, a_rows - 1) * p.sfa_sm) * 4u;
+        }
+    }
+    auto issue_a = [&](int kb, int st) {
+        kb = min(kb, num_kb - 1);   // past the end: reload the last block into the free slot
+        const uint32_t lds = a_ring + st * A_STAGE;
+        const uint8_t* base = a_p + (int64_t)kb * kBK;
+        const uint8_t* sa_kb = reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk);
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+            const int e = min(i * AS + iw, A_LOADS - 1);   // wave-uniform
+            if (e < A_SEGS)
+                dma16_saddr(base, voff_a[i], lds + e * 1024);
+            else
+                dma4_saddr(sa_kb, voff_a[i], lds + ROWS * kBK + (e - A_SEGS) * 256);
+        }
+    };
+    auto issue_b = [&](int kb, int st) {
+        S::template issue<LB, BLS::BS>(b_t, voff_b, num_kb, kb, st, iw, smem_lds);
+    };
+
+    // Prologue B(0), B(1) (unless in flight already), A(0 .. SA-2); wait until
+    // only A(1 .. SA-2) may be in flight.
+    if (NL == 0 || loader) {
+        if (!b_primed) {
+            issue_b(0, 0);
+            issue_b(1, 1);
+        }
+#pragma unroll
+        for (int s = 0; s < SA - 1; ++s) issue_a(s, s);
+    }
+    wait_vmcnt_barrier<(SA - 2) * LA>();
+
+    if (loader) {
+        // The slots refilled at block kb held K block kb - 1, which every compute
+        // wave finished before the last barrier.
+        for (int kb = 0; kb < num_kb; ++kb) {
+            issue_a(kb + SA - 1, (kb + SA - 1) % SA);
+            issue_b(kb + 2, (kb + 2) % 3);
+            wait_vmcnt_barrier<W>();
+        }
+        // No stage load may still be writing LDS when the epilogue reuses it.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        return;
+    }
 
     // Fragment reads: lane (lrow, lhalf) takes row r0 + lrow, logical chunks
     // 4ks + 2lhalf and 4ks + 2lhalf + 1 (K bytes [64ks + 32lhalf, +32)).
@@ -153,39 +245,6 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
         const i32x4 hi = *reinterpret_cast<const i32x4*>(slab + frag_off[ks][1]);
         return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
-
-    const uint8_t* __restrict__ a_p = p.a + (int64_t)g * p.a_gs + (int64_t)r0 * p.lda;
-    const float* __restrict__ sa_p = p.sfa + (int64_t)g * p.sfa_gs + (int64_t)r0 * p.sfa_sm;
-
-    // Per-lane offsets of the wave's A stage loads (entry e = i * NW + wave of the
-    // list): rows past a_rows repeat the last valid one, whose outputs are never
-    // stored.
-    uint32_t voff_a[LA];
-#pragma unroll
-    for (int i = 0; i < LA; ++i) {
-        const int e = min(i * NW + wave, A_LOADS - 1);
-        if (e < A_SEGS) {
-            const int row = e * 8 + rs;
-            voff_a[i] = (uint32_t)min(row, a_rows - 1) * (uint32_t)p.lda + ((pc ^ swz_g(row)) << 4);
-        } else {
-            voff_a[i] = (uint32_t)(min((e - A_SEGS) * 64 + lane, a_rows - 1) * p.sfa_sm) * 4u;
-        }
-    }
-    auto issue_a = [&](int kb, int st) {
-        kb = min(kb, num_kb - 1);   // past the end: reload the last block into the free slot
-        const uint32_t lds = a_ring + st * A_STAGE;
-        const uint8_t* base = a_p + (int64_t)kb * kBK;
-        const uint8_t* sa_kb = reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk);
-#pragma unroll
-        for (int i = 0; i < LA; ++i) {
-            const int e = min(i * NW + wave, A_LOADS - 1);   // wave-uniform
-            if (e < A_SEGS)
-                dma16_saddr(base, voff_a[i], lds + e * 1024);
-            else
-                dma4_saddr(sa_kb, voff_a[i], lds + ROWS * kBK + (e - A_SEGS) * 256);
-        }
-    };
-    auto issue_b = [&](int kb, int st) { S::issue(b_t, voff_b, num_kb, kb, st, wave, smem_lds); };
     // The wave's SFB column (its 32 columns lie in one 128-row group), read with
     // scalar loads one K block ahead.
     cfloat* sfb_w = (cfloat*)(p.sfb + (int64_t)g * p.sfb_gs +
@@ -198,15 +257,6 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
 #pragma unroll
         for (int e = 0; e < 16; ++e) fin[i][0][e] = 0.f;
 
-    // Prologue B(0), B(1) (unless in flight already), A(0 .. SA-2); wait until
-    // only A(1 .. SA-2) may be in flight.
-    if (!b_primed) {
-        issue_b(0, 0);
-        issue_b(1, 1);
-    }
-#pragma unroll
-    for (int s = 0; s < SA - 1; ++s) issue_a(s, s);
-    wait_vmcnt_barrier<(SA - 2) * LA>();
     for (int kb = 0; kb < num_kb; ++kb) {
         // The slots refilled here held K block kb - 1, which every wave finished
         // before the last barrier.
@@ -216,6 +266,28 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
         const i32x8 ob0 = frag(b_tile, wave * 32, 0), ob1 = frag(b_tile, wave * 32, 1);
         const float sb = sb_next;
         sb_next = sfb_w[(int64_t)min(kb + 1, num_kb - 1) * p.sfb_sk];
+        if constexpr (NL > 0) {
+            // Three waves per SIMD leave 168 registers: one A fragment and one
+            // accumulator. Row tile rt + 1's fragment is read right after rt's
+            // MFMA pair has issued, and rt is promoted as soon as its pair is
+            // done; the SIMD's other compute wave fills the matrix core meanwhile.
+            i32x8 oa0 = frag(a_tile, 0, 0), oa1 = frag(a_tile, 0, 1);
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                const float sa = *reinterpret_cast<const float*>(a_tile + ROWS * kBK + (rt * 32 + lrow) * 4);
+                const f32x16 c =
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ob0, oa0, f32x16{}, 0, 0, 0, 0, 0, 0);
+                const f32x16 acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ob1, oa1, c, 0, 0, 0, 0, 0, 0);
+                if (rt + 1 < NRT) {
+                    oa0 = frag(a_tile, (rt + 1) * 32, 0);
+                    oa1 = frag(a_tile, (rt + 1) * 32, 1);
+                }
+                const float scl = sa * sb;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) fin[rt][0][e] = __builtin_fmaf(scl, acc[e], fin[rt][0][e]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
         // Row tile rt + 1's A fragment is read while rt's MFMA pair runs, and rt's
         // pair is issued before rt - 1 is promoted, so LDS reads and FMAs overlap
         // the matrix core. (The scheduling barriers keep the compiler from
@@ -239,10 +311,13 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
                                                                               0);
                 scl[rt & 1] = sa * sb;
             }
+            // the wave's share of the stage loads: A after the first MFMA pair,
+            // then one B load per row tile
             if (rt == 0) issue_a(kb + SA - 1, (kb + SA - 1) % SA);
 #pragma unroll
             for (int i = 0; i < LB; ++i)
-                if (min(1 + i, NRT) == rt) S::issue_one(b_t, voff_b, num_kb, kb + 2, (kb + 2) % 3, wave, smem_lds, i);
+                if (min(1 + i, NRT) == rt)
+                    S::template issue_one<LB, BLS::BS>(b_t, voff_b, num_kb, kb + 2, (kb + 2) % 3, iw, smem_lds, i);
             if (rt >= 1) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
@@ -250,8 +325,11 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        }
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt_barrier<W>();
+        // (compute waves of a pass with loaders issue no vector loads: the count
+        // is then 0 and the wait is for the LDS reads only)
+        wait_vmcnt_barrier<NL ? 0 : W>();
     }
     // No stage load may still be writing LDS when the epilogue reuses it.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -312,7 +390,7 @@ __device__ __forceinline__ void masked_pass16(const Fp8GemmArgs& p, uint8_t* sme
         else
             dma4_saddr(reinterpret_cast<const uint8_t*>(sa_p + (int64_t)kb * p.sfa_sk), voff_a, lds + ROWS * kBK);
     };
-    auto issue_b = [&](int kb, int st) { S::issue(b_t, voff_b, num_kb, kb, st, wave, smem_lds); };
+    auto issue_b = [&](int kb, int st) { S::template issue<LB, NW>(b_t, voff_b, num_kb, kb, st, wave, smem_lds); };
     cfloat* sfb_w = (cfloat*)(p.sfb + (int64_t)g * p.sfb_gs +
                               (int64_t)min((n0 + wave * 32) >> 7, (p.n - 1) >> 7) * p.sfb_sn);
     float sb_next = sfb_w[0];
@@ -390,11 +468,14 @@ __device__ __forceinline__ void masked_pass16(const Fp8GemmArgs& p, uint8_t* sme
 
 // M16: passes of at most 16 rows take the 16 x 16 x 128 pass (a separate
 // instantiation, so the 32-row passes keep their register allocation when it is off).
-template <int NW, int M16>
-__global__ void __launch_bounds__(NW * 64, 1)
+// NL: loader waves of the 32-row passes (launched with NW + NL waves; not with M16).
+template <int NW, int M16, int NL>
+__global__ void __launch_bounds__((NW + NL) * 64, 1)
 fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
     static_assert(NW >= 4 && NW <= 8, "4 to 8 waves");
+    static_assert(!(M16 && NL), "the 16-row pass has no loader waves");
     using S = StreamShape<NW>;
+    using BLS = BList<NW, NL>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
 
     const int tid = threadIdx.x;
@@ -404,14 +485,19 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
     const int g = lt / num_n_tiles;
     const int n0 = (lt - g * num_n_tiles) * S::BN;
     const int num_kb = p.k / kBK;
+    // the waves that issue stage loads: all of them, or the loaders
+    const bool issuer = NL == 0 || wave >= NW;
+    const int iw = NL ? max(wave - NW, 0) : wave;
 
     // The first two B stages do not depend on masked_m: start them before it is read.
     const uint8_t* __restrict__ b_t = p.b + (int64_t)g * p.b_gs + (int64_t)n0 * p.ldb;
-    uint32_t voff_b[S::LB];
-    S::offsets(voff_b, wave, lane >> 3, lane & 7, min(S::BN, p.n - n0), p.ldb);
+    uint32_t voff_b[BLS::BL];
+    S::template offsets<BLS::BL, BLS::BS>(voff_b, iw, lane >> 3, lane & 7, min(S::BN, p.n - n0), p.ldb);
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
-    S::issue(b_t, voff_b, num_kb, 0, 0, wave, smem_lds);
-    S::issue(b_t, voff_b, num_kb, 1, 1, wave, smem_lds);
+    if (issuer) {
+        S::template issue<BLS::BL, BLS::BS>(b_t, voff_b, num_kb, 0, 0, iw, smem_lds);
+        S::template issue<BLS::BL, BLS::BS>(b_t, voff_b, num_kb, 1, 1, iw, smem_lds);
+    }
 
     // masked_m (a dense call runs as one group of all p.m rows, layout = null)
     const int m_g = p.layout ? min(((const __attribute__((address_space(4))) int32_t*)p.layout)[g], p.m) : p.m;
@@ -431,11 +517,11 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
             }
         }
         switch (nrt) {
-            case 1: masked_pass<NW, 1>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            case 2: masked_pass<NW, 2>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            case 3: masked_pass<NW, 3>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            case 4: masked_pass<NW, 4>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            default: masked_pass<NW, 5>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 1: masked_pass<NW, 1, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 2: masked_pass<NW, 2, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 3: masked_pass<NW, 3, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 4: masked_pass<NW, 4, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            default: masked_pass<NW, 5, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
         }
     }
 }
@@ -448,11 +534,11 @@ void launch_nw(const Fp8GemmArgs& a, int mfma16, hipStream_t stream) {
     if (grid == 0) return;
     DG_CHECK(grid < (int64_t)1 << 31);
     if (mfma16)
-        hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 1>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
-                           num_n_tiles);
+        hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 1, 0>), dim3((unsigned)grid), dim3(NW * 64), 0, stream,
+                           a, num_n_tiles);
     else
-        hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 0>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a,
-                           num_n_tiles);
+        hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 0, kMaskedLoaders>), dim3((unsigned)grid),
+                           dim3((NW + kMaskedLoaders) * 64), 0, stream, a, num_n_tiles);
     DG_HIP_CHECK(hipGetLastError());
 }
 
