@@ -360,7 +360,7 @@ bool is_1d1d(const Operands& o, const Recipe& r) {
            r.gran_k_b == 128;
 }
 
-// The 1D1D kernels: the 256 x 128 LDS-pipelined one (variant 7, the default) or
+// The 1D1D kernels: the 128 x 128 LDS-pipelined one (variant 7, the default) or
 // the 128-row streaming one (variant 6, by tile override).
 void launch_1d1d(bool k_grouped, const Fp8GemmArgs& args, hipStream_t stream, int64_t m, int64_t n, int64_t k,
                  int64_t groups) {
@@ -371,7 +371,7 @@ void launch_1d1d(bool k_grouped, const Fp8GemmArgs& args, hipStream_t stream, in
         launch_fp8_gemm_1d1d(k_grouped, waves, args, stream);
         return;
     }
-    record_config("fp8_gemm_1d1d", kind, TileConfig{256, 128, 7}, m, n, k, groups);
+    record_config("fp8_gemm_1d1d", kind, TileConfig{128, 128, 7}, m, n, k, groups);
     launch_fp8_gemm_1d1d_pipe(k_grouped, args, stream);
 }
 
@@ -1229,7 +1229,7 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
                                           block_n % 32 == 0 && block_n >= 128 &&
                                           block_n <= 256)
                         : variant == 6 ? (block_m == 128 && (block_n == 128 || block_n == 192 || block_n == 256))
-                        : variant == 7 ? (block_m == 256 && block_n == 128)
+                        : variant == 7 ? (block_m == 128 && block_n == 128)
                         : variant == 8 || variant == 9
                             ? (block_m == kTinyMRows && (block_n == 16 || block_n == 32 || block_n == 64))
                                        : (variant == 4 && block_m == 256 && block_n == 256);

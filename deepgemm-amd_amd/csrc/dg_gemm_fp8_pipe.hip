@@ -72,7 +72,8 @@ __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2))
 // into a three-slot LDS ring, and the stages carry no SFA.
 template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT, int PERSIST,
           int SB1D = 0, int KSA = 0>
-__global__ void __launch_bounds__(WGM * WGN * 64, 1)
+// (Four-wave 1D1D tiles run two workgroups per CU: at most 256 registers.)
+__global__ void __launch_bounds__(WGM * WGN * 64, (WGM * WGN == 4 && SB1D) ? 2 : 1)
 fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const int num_n_blocks,
                           const int raster_gm) {
     constexpr int NW = WGM * WGN;              // waves per workgroup (4: one per SIMD, 8: two per SIMD)
@@ -700,12 +701,14 @@ void launch_tile(GemmKind kind, const Fp8GemmArgs& a, hipStream_t stream) {
 // each group's K) a multiple of 128.
 template <int KIND>
 void launch_1d1d_kind(const Fp8GemmArgs& a, hipStream_t stream) {
-    // 256 x 128 with eight waves of 64 x 64 (231 registers, two waves per SIMD, so
-    // one wave's promotion, twice the VALU work of the 1D2D recipe's, runs under
-    // the other's MFMAs): the per-column scales (16 more live registers per
-    // sub-tile column) do not fit the 256 registers of the eight-wave 256 x 256
-    // tile.
-    constexpr int BM = 256, BN = 128;
+    // 128 x 128 with four waves of 64 x 64 and two stages (217 registers, 68.6 KB
+    // of LDS), so two workgroups share a CU: one's FP32 C/D epilogue, a burst of
+    // HBM traffic with the matrix core idle, runs under the other's K loop
+    // (K-grouped, 8 x 4096 x 7168: 2.02-2.06 ms against 2.17-2.18 ms for 256 x 128
+    // with eight waves and three stages, one workgroup per CU). The per-column
+    // scales (16 more live registers per sub-tile column) do not fit the 256
+    // registers of the eight-wave 256 x 256 tile.
+    constexpr int BM = 128, BN = 128;
     const int num_n_blocks = (a.n + BN - 1) / BN;
     const int num_m_blocks = (a.m + BM - 1) / BM;
     int64_t grid = (int64_t)num_m_blocks * num_n_blocks;
@@ -714,8 +717,8 @@ void launch_1d1d_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     DG_CHECK(grid < (int64_t)1 << 31);
     DG_CHECK(a.out_f32 && a.c != nullptr && a.k % kBK == 0);
     const int raster_gm = choose_raster_gm(BM, BN, num_m_blocks);
-    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, 4, 2, 3, KIND, 1, 1, 0, 0, 1>), dim3((unsigned)grid),
-                       dim3(512), 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+    hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, 2, 2, 2, KIND, 1, 1, 0, 0, 1>), dim3((unsigned)grid),
+                       dim3(256), 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
     DG_HIP_CHECK(hipGetLastError());
 }
 
