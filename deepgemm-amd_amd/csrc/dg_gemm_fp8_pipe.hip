@@ -268,9 +268,28 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const uint32_t voff_sa = (uint32_t)(min(sa_row, a_rows - 1) * p.sfa_sm) * 4u;
     const int sb_seg = min(wave, SB_SEGS - 1);   // SB1D: surplus waves repeat the last segment
     const uint32_t voff_sb = SB1D ? (uint32_t)(min(sb_seg * 64 + lane, b_rows - 1) * p.sfb_sn) * 4u : 0u;
-    auto clamped_voff = [&](int seg, int rows, int ld) {
-        const int r = min(seg * 8 + launder(rs), rows - 1);
-        return (uint32_t)r * (uint32_t)ld + chunk_off;
+    // Fast-path load of segment seg (8 rows): the segment's first row goes into the
+    // wave-uniform SGPR base (clamped to the last valid row), and the lane adds its
+    // own row and chunk, vlane = rs * ld + chunk_off, a loop-invariant register.
+    // Lanes past the last valid row are clamped by one v_min_u32 against a uniform
+    // limit, the last valid row's final chunk: they load bytes of that row, which
+    // only feed outputs past the edge (never stored). The limit is laundered so the
+    // per-segment minimum is recomputed at each issue instead of being held in a
+    // register across the loop.
+    const uint32_t vlane_a = (uint32_t)rs * (uint32_t)lda + chunk_off;
+    const uint32_t vlane_b = (uint32_t)rs * (uint32_t)ldb + chunk_off;
+    auto seg_load = [&](const uint8_t* kb_base, int seg, int rows, int64_t ld, uint32_t vlane, uint32_t lds) {
+        if constexpr (KIND == kContiguous) {
+            // (the contiguous tiles' two-pass form spills with the SGPR form; they
+            // keep per-lane offsets computed at issue time)
+            const int r = min(seg * 8 + launder(rs), rows - 1);
+            dma16_saddr(kb_base, (uint32_t)r * (uint32_t)ld + chunk_off, lds);
+            return;
+        }
+        const int rb = min(seg * 8, rows - 1);
+        uint32_t lim = (uint32_t)(rows - 1 - rb) * (uint32_t)ld + (uint32_t)(kBK - 16);
+        asm volatile("" : "+s"(lim));
+        dma16_saddr(kb_base + (int64_t)rb * ld, min(vlane, lim), lds);
     };
 
     const uint32_t smem_lds = __builtin_amdgcn_readfirstlane(lds_address(smem));
@@ -286,13 +305,26 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const uint32_t sag_lds = __builtin_amdgcn_readfirstlane(lds_address(reinterpret_cast<const uint8_t*>(&s_sag[0][0][0])));
     const int ksa_last = KSA ? num_kb / (KSA ? KSA : 1) - 1 : 0;
     const uint64_t seg_exec = KSA ? (0xFFull << (8 * wave)) : 0ull;
-    // segment j of group g (only this wave's 8 lanes when `whole` is false)
+    // segment j of group g (only this wave's 8 lanes when `whole` is false); rows
+    // are clamped as in seg_load: the segment's first row in the SGPR base, the
+    // lane's row and 16-byte part in a loop-invariant register, one v_min_u32.
+    const uint32_t sag_row_bytes = (uint32_t)p.sfa_sm * 4u;
+    const uint32_t vlane_sag = (uint32_t)(lane / KSA_LPR) * sag_row_bytes + (lane % KSA_LPR) * 16u;
     auto issue_segment = [&](int g, int j, bool whole) {
-        const int row = j * KSA_RPS + launder(lane) / KSA_LPR;
-        const uint32_t voff = (uint32_t)(min(row, a_rows - 1) * p.sfa_sm) * 4u + (lane % KSA_LPR) * 16u;
+        if constexpr (KIND == kContiguous) {   // (per-lane offsets, as in seg_load)
+            const int row = j * KSA_RPS + launder(lane) / KSA_LPR;
+            const uint32_t voff = (uint32_t)(min(row, a_rows - 1) * p.sfa_sm) * 4u + (lane % KSA_LPR) * 16u;
+            dma16_saddr_masked(whole ? __builtin_amdgcn_read_exec() : seg_exec,
+                               reinterpret_cast<const uint8_t*>(sa_base + KSA * g), voff,
+                               sag_lds + (g % 3) * (BM * KSA * 4) + j * 1024);
+            return;
+        }
+        const int rb = min(j * KSA_RPS, a_rows - 1);
+        uint32_t lim = (uint32_t)(a_rows - 1 - rb) * sag_row_bytes + (KSA_LPR - 1) * 16u;
+        asm volatile("" : "+s"(lim));
         dma16_saddr_masked(whole ? __builtin_amdgcn_read_exec() : seg_exec,
-                           reinterpret_cast<const uint8_t*>(sa_base + KSA * g), voff,
-                           sag_lds + (g % 3) * (BM * KSA * 4) + j * 1024);
+                           reinterpret_cast<const uint8_t*>(sa_base + KSA * g + (int64_t)rb * p.sfa_sm),
+                           min(vlane_sag, lim), sag_lds + (g % 3) * (BM * KSA * 4) + j * 1024);
     };
     // the load at the top of block kb (kb = -1: before the loop)
     auto issue_block_segment = [&](int kb) {
@@ -310,14 +342,14 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
 #pragma unroll
             for (int i = 0; i < A_INSTR; ++i) {
                 const int seg = i * NW + wave;
-                dma16_saddr(a_kb, clamped_voff(seg, a_rows, lda), stage_lds + seg * 1024);
+                seg_load(a_kb, seg, a_rows, lda, vlane_a, stage_lds + seg * 1024);
             }
             }
             if (part != 1) {
 #pragma unroll
             for (int i = 0; i < B_INSTR; ++i) {
                 const int seg = i * NW + wave;
-                dma16_saddr(b_kb, clamped_voff(seg, b_rows, ldb), stage_lds + BM * kBK + seg * 1024);
+                seg_load(b_kb, seg, b_rows, ldb, vlane_b, stage_lds + BM * kBK + seg * 1024);
             }
             }
             if constexpr (!KSA)
