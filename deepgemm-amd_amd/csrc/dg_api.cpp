@@ -327,6 +327,34 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     return out;
 }
 
+// Column split of a dense call whose 256 x 256 tiles leave the last round partly
+// empty (4096 x 7168: 448 tiles, 1.75 rounds on 256 CUs, so the second round
+// leaves 64 CUs idle): columns [0, n1) run as 256 x 256 tiles in whole rounds
+// and [n1, n) as 256 x 192 tiles (4096 x 7168: one round of each, 256 x 256
+// over 4096 columns and 256 x 192 over 3072). Every tile computes its outputs
+// with the same arithmetic, so the result is bitwise that of one launch.
+// Returns n1, or 0 when the per-round cost model (the heuristic's measured
+// tile throughputs) gains less than 5% (the second launch has a fixed cost), or
+// K is under 4096. A part-empty round is cheaper than the model says: with 192
+// of 256 CUs busy the clock rises (2.35 against 2.14-2.18 GHz under full MFMA
+// load) and each tile runs ~22% faster, so the split measured -2.5% at
+// 4096 x 7168 x 16384 (-4.6% with FP32 C) but +7% at K = 2048 with FP32 C,
+// where the second launch's start and its C epilogue outweigh it.
+int64_t dense_split_columns(int64_t m_rows, int64_t n, int64_t k, int cus) {
+    if (k < 4096) return 0;
+    constexpr double t256 = 256.0 * 256 / 1.32, t192 = 256.0 * 192 / 1.16;   // per-round cost of each tile
+    const int64_t mb = ceil_div(m_rows, 256);
+    auto rounds = [&](int64_t tiles) { return (double)ceil_div(tiles, (int64_t)cus); };
+    const double whole = rounds(mb * ceil_div(n, 256)) * t256;
+    double best = whole;
+    int64_t best_n1 = 0;
+    for (int64_t n1 = 256; n1 < n; n1 += 256) {
+        const double cost = rounds(mb * (n1 / 256)) * t256 + rounds(mb * ceil_div(n - n1, 192)) * t192;
+        if (cost < best - 1e-9) best = cost, best_n1 = n1;
+    }
+    return best < 0.95 * whole ? best_n1 : 0;
+}
+
 void record_config(const char* kernel, GemmKind kind, const TileConfig& t, int64_t m, int64_t n, int64_t k,
                    int64_t g) {
     char buf[256];
@@ -473,6 +501,25 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
         record_config("fp8_gemm_1d2d", kind, t, m, n, k, groups);
+        if (kind == kNormal && tv == 0 && t.variant == 2 && t.block_m == 256 && t.block_n == 256) {
+            const int64_t n1 = dense_split_columns(m_rows, n, k, args.grid_limit);
+            if (n1 > 0) {
+                t_last_config += " split_n=" + std::to_string(n1) + ":256x192";
+                Fp8GemmArgs lo = args;
+                lo.n = (int32_t)n1;
+                launch_fp8_gemm_1d2d_v2(kind, t, lo, stream);
+                // columns [n1, n): B rows, SFB rows (n1 is a multiple of 128), D and C columns
+                Fp8GemmArgs hi = args;
+                hi.n = (int32_t)(n - n1);
+                hi.b = args.b + n1 * args.ldb;
+                hi.sfb = args.sfb + (n1 / 128) * args.sfb_sn;
+                const int64_t elem = args.out_f32 ? 4 : 2;
+                hi.d = static_cast<uint8_t*>(args.d) + n1 * elem;
+                if (args.c) hi.c = static_cast<const uint8_t*>(args.c) + n1 * elem;
+                launch_fp8_gemm_1d2d_v2(kind, TileConfig{256, 192, 2}, hi, stream);
+                return;
+            }
+        }
         if (t.variant == 8 || t.variant == 9)
             launch_fp8_gemm_tinym(args, t.variant == 8 ? 8 : 4, t.block_n, stream);
         else if (t.variant == 5)

@@ -100,6 +100,48 @@ def test_all_tiles_bitwise_equal(m, n, k):
         assert torch.equal(o.view(torch.int16), outs[0][1].view(torch.int16))
 
 
+@pytest.mark.parametrize('m,n,k,acc', [(4096, 7168, 4096, False), (4096, 7168, 4096, True), (8192, 7168, 4096, False)])
+def test_dense_column_split_equals_one_launch(m, n, k, acc):
+    """Dense calls (K >= 4096) whose 256 x 256 tiles would leave the last round part
+    empty run as two launches (256 x 256 tiles over the first columns, 256 x 192 over the rest):
+    bitwise the single 256 x 256 launch, BF16 out and FP32 C in place, and the
+    split rows and columns hold the oracle's values."""
+    print(f'dense column split m={m} n={n} k={k} acc={acc}', flush=True)
+    x = gen.dense_inputs(m, n, k, seed=21)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    c_np = gen.randn_bf16((m, n), 23) * 32.0 if acc else None
+
+    def run():
+        if acc:
+            d = f32(c_np)
+            deep_gemm.fp8_gemm_nt(a, b, d, c=d)
+        else:
+            d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+            deep_gemm.fp8_gemm_nt(a, b, d)
+        return d, deep_gemm.get_last_config()
+
+    split, cfg = run()
+    print(cfg, flush=True)
+    assert 'split_n=' in cfg, cfg
+    try:
+        deep_gemm.set_tile_override(256, 256, variant=2)
+        whole, cfg1 = run()
+        assert 'split_n=' not in cfg1, cfg1
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(split.view(torch.int32 if acc else torch.int16), whole.view(torch.int32 if acc else torch.int16))
+    # rows on both sides of the split column, against the oracle
+    n1 = int(cfg.split('split_n=')[1].split(':')[0])
+    rows = np.array([0, 1, 255, 256, 2047, m - 1])
+    cols = np.r_[0:8, n1 - 8:n1 + 8, n - 8:n]
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'][rows], x['sfa'][rows]),
+                        oquant.dequant_per_block(x['qb'], x['sfb']), None if c_np is None else c_np[rows])
+    out = split.float().cpu().numpy()[rows]
+    diff, _ = report('column split', out[:, cols], ref[:, cols])
+    assert diff < 1e-5
+
+
 @pytest.mark.parametrize('inplace', [True, False])
 def test_dense_c_accumulate_f32(inplace):
     m, n, k = 256, 384, 896
