@@ -55,12 +55,25 @@ def _short(name: str) -> str:
     return name
 
 
-def phase_slices(num_launches: int, steps: int, rot: int):
+def phase_slices(num_launches: int, steps: int, rot: int, disp=None):
     """Index ranges, within the library dispatch sequence, of each launch's
-    per-launch timing dispatches (repetitions x rotating sets)."""
+    per-launch timing dispatches (repetitions x rotating sets x the launch's
+    dispatches per call), and the calls per launch in that phase. `disp[i]` is
+    the number of kernels one call of launch i dispatches (2 for a dense column
+    split, else 1)."""
+    disp = disp or [1] * num_launches
     per = max(5, steps) * rot
-    base = rot * num_launches
-    return [range(base + i * per, base + (i + 1) * per) for i in range(num_launches)], per
+    start = rot * sum(disp)
+    out = []
+    for d in disp:
+        out.append(range(start, start + per * d))
+        start += per * d
+    return out, per
+
+
+def dispatches_per_call(config: str) -> int:
+    """Kernels one library call dispatches: a dense column split runs two."""
+    return 2 if 'split_n=' in config else 1
 
 
 def read_trace(path):
@@ -96,24 +109,28 @@ def summarize(args):
     warmup = args.warmup if args.warmup is not None else bench['warmup']
     steps = args.steps if args.steps is not None else bench['steps']
     rot = bench.get('timing', {}).get('rotating_sets', 1)
-    slices, reps = phase_slices(len(names), steps, rot)
+    disp = [dispatches_per_call(roof.get('launch_config', {}).get(n, '')) for n in names]
+    slices, reps = phase_slices(len(names), steps, rot, disp)
 
     trace = read_trace(args.trace)
     seq = gemm_sequence([(int(r['Dispatch_Id']), r['Kernel_Name'], r) for r in trace])
-    expected = (rot + warmup + steps) * len(names) + reps * len(names)
+    expected = (rot + warmup + steps) * sum(disp) + reps * sum(disp)
     if len(seq) != expected:
         sys.exit(f'expected {expected} library dispatches (warmup {warmup}, steps {steps}, '
-                 f'{rot} rotating sets, {len(names)} launches), found {len(seq)}')
+                 f'{rot} rotating sets, {len(names)} launches, {sum(disp)} dispatches per step), found {len(seq)}')
     per = []
-    for name, sl in zip(names, slices):
+    for name, sl, d in zip(names, slices, disp):
         rows = [seq[i][2] for i in sl]
         kern = {_short(r['Kernel_Name']) for r in rows}
-        durs = [(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3 for r in rows]
+        # one call = d consecutive dispatches: first start to last end
+        durs = [(int(rows[c + d - 1]['End_Timestamp']) - int(rows[c]['Start_Timestamp'])) / 1e3
+                for c in range(0, len(rows), d)]
         r0 = rows[0]
-        per.append({'launch': name, 'kernel': ' / '.join(sorted(kern)), 'calls': len(rows),
+        grids = [int(rows[j]['Grid_Size_X']) // max(1, int(rows[j]['Workgroup_Size_X'])) for j in range(d)]
+        per.append({'launch': name, 'kernel': ' / '.join(sorted(kern)), 'calls': len(durs),
                     'avg_us': sum(durs) / len(durs), 'min_us': min(durs), 'max_us': max(durs),
                     'event_us': roof['per_launch_us'][name],
-                    'grid': int(r0['Grid_Size_X']) // max(1, int(r0['Workgroup_Size_X'])),
+                    'grid': grids[0] if d == 1 else '+'.join(str(g) for g in grids),
                     'vgpr': int(r0['VGPR_Count']), 'agpr': int(r0['Accum_VGPR_Count']),
                     'lds': int(r0['LDS_Block_Size'])})
 
@@ -132,12 +149,12 @@ def summarize(args):
                               'factor': factor}
             gseq = gemm_sequence([(d, n, v) for d, (n, v) in vals.items()])
             # Under --pmc bench.py runs with the warmup/steps given on the command line.
-            psl, preps = phase_slices(len(names), args.pmc_steps, rot)
-            exp = (rot + args.pmc_warmup + args.pmc_steps) * len(names) + preps * len(names)
+            psl, preps = phase_slices(len(names), args.pmc_steps, rot, disp)
+            exp = (rot + args.pmc_warmup + args.pmc_steps) * sum(disp) + preps * sum(disp)
             if len(gseq) != exp:
                 sys.exit(f'{path}: expected {exp} library dispatches, found {len(gseq)}')
-            for name, sl in zip(names, psl):
-                kib = sum(gseq[i][2] for i in sl) / len(sl)
+            for name, sl, d in zip(names, psl, disp):
+                kib = sum(gseq[i][2] for i in sl) / (len(sl) / d)   # per call
                 traffic.setdefault(name, {})[counter] = kib * 1024.0 / factor
         traffic = {'per_launch_bytes': {n: {'fetch': round(t['FETCH_SIZE']), 'write': round(t['WRITE_SIZE']),
                                             'total': round(t['FETCH_SIZE'] + t['WRITE_SIZE'])}
@@ -152,11 +169,11 @@ def summarize(args):
         gui = read_counters(args.mfma, 'GRBM_GUI_ACTIVE')
         bseq = gemm_sequence([(d, n, v) for d, (n, v) in busy.items()])
         gseq2 = gemm_sequence([(d, n, v) for d, (n, v) in gui.items()])
-        psl, _ = phase_slices(len(names), args.pmc_steps, rot)
+        psl, _ = phase_slices(len(names), args.pmc_steps, rot, disp)
         mfma = {}
-        for name, sl, p in zip(names, psl, per):
-            b = sum(bseq[i][2] for i in sl) / len(sl)
-            cyc = sum(gseq2[i][2] for i in sl) / len(sl) / args.xcds
+        for name, sl, p, d in zip(names, psl, per, disp):
+            b = sum(bseq[i][2] for i in sl) / (len(sl) / d)   # per call
+            cyc = sum(gseq2[i][2] for i in sl) / (len(sl) / d) / args.xcds
             mfma[name] = {'mfma_busy_frac': b / (cyc * args.simds), 'clock_ghz': cyc / (p['avg_us'] * 1e3)}
 
     lines = []
