@@ -682,7 +682,12 @@ def test_persistent_equals_per_tile_launch(case):
 
 # ----------------------------------------------------------------- SF layouts
 
-@pytest.mark.parametrize('mn,k,g', [(4096, 7168, 1), (4097, 128, 2), (300, 7296, 4)])
+# the reference's grid (tests/generators.py:276-285, tests/test_layout.py:45-80), plus a ragged mn
+SF_LAYOUT_CASES = [(mn, k, g) for mn in (4096, 4097, 8192) for k in (128, 7168, 7296) for g in (1, 2, 4)] + \
+                  [(300, 7296, 4)]
+
+
+@pytest.mark.parametrize('mn,k,g', SF_LAYOUT_CASES)
 def test_sf_transpose_and_pack(mn, k, g):
     sfk = (k + 127) // 128
     rng = np.random.default_rng(mn + k)
