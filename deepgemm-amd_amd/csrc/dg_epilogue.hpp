@@ -177,8 +177,11 @@ struct RowEpilogue {
                 if constexpr (ES == 2 && !HAS_C) {
                     // staged bf16 is the output: copy the bytes
                     if (full_chunk(n, n_total) && store) {
-                        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(d) + d_goff + (int64_t)m * ldd + n) =
-                            *reinterpret_cast<const uint4*>(region + r * ROW_BYTES + (unit(r, byte >> 4) << 4));
+                        // D is written once and never read back by the kernel: a
+                        // non-temporal store keeps it from displacing operands in L2
+                        __builtin_nontemporal_store(
+                            *reinterpret_cast<const i32x4*>(region + r * ROW_BYTES + (unit(r, byte >> 4) << 4)),
+                            reinterpret_cast<i32x4*>(static_cast<uint16_t*>(d) + d_goff + (int64_t)m * ldd + n));
                         continue;
                     }
                 }
@@ -202,7 +205,7 @@ struct RowEpilogue {
                         }
                     }
                     if (full) {
-                        *reinterpret_cast<f32x4*>(dp) = f32x4{v[0], v[1], v[2], v[3]};
+                        __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(dp));
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
@@ -227,8 +230,10 @@ struct RowEpilogue {
                         }
                     }
                     if (full) {
-                        *reinterpret_cast<uint4*>(dp) = uint4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                                              pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+                        __builtin_nontemporal_store(
+                            i32x4{(int)pack_bf16x2(v[0], v[1]), (int)pack_bf16x2(v[2], v[3]),
+                                  (int)pack_bf16x2(v[4], v[5]), (int)pack_bf16x2(v[6], v[7])},
+                            reinterpret_cast<i32x4*>(dp));
                     } else {
 #pragma unroll
                         for (int e = 0; e < 8; ++e)
