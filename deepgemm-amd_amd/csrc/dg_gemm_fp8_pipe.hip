@@ -279,13 +279,6 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const uint32_t vlane_a = (uint32_t)rs * (uint32_t)lda + chunk_off;
     const uint32_t vlane_b = (uint32_t)rs * (uint32_t)ldb + chunk_off;
     auto seg_load = [&](const uint8_t* kb_base, int seg, int rows, int64_t ld, uint32_t vlane, uint32_t lds) {
-        if constexpr (KIND == kContiguous) {
-            // (the contiguous tiles' two-pass form spills with the SGPR form; they
-            // keep per-lane offsets computed at issue time)
-            const int r = min(seg * 8 + launder(rs), rows - 1);
-            dma16_saddr(kb_base, (uint32_t)r * (uint32_t)ld + chunk_off, lds);
-            return;
-        }
         const int rb = min(seg * 8, rows - 1);
         uint32_t lim = (uint32_t)(rows - 1 - rb) * (uint32_t)ld + (uint32_t)(kBK - 16);
         asm volatile("" : "+s"(lim));
@@ -311,14 +304,6 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const uint32_t sag_row_bytes = (uint32_t)p.sfa_sm * 4u;
     const uint32_t vlane_sag = (uint32_t)(lane / KSA_LPR) * sag_row_bytes + (lane % KSA_LPR) * 16u;
     auto issue_segment = [&](int g, int j, bool whole) {
-        if constexpr (KIND == kContiguous) {   // (per-lane offsets, as in seg_load)
-            const int row = j * KSA_RPS + launder(lane) / KSA_LPR;
-            const uint32_t voff = (uint32_t)(min(row, a_rows - 1) * p.sfa_sm) * 4u + (lane % KSA_LPR) * 16u;
-            dma16_saddr_masked(whole ? __builtin_amdgcn_read_exec() : seg_exec,
-                               reinterpret_cast<const uint8_t*>(sa_base + KSA * g), voff,
-                               sag_lds + (g % 3) * (BM * KSA * 4) + j * 1024);
-            return;
-        }
         const int rb = min(j * KSA_RPS, a_rows - 1);
         uint32_t lim = (uint32_t)(a_rows - 1 - rb) * sag_row_bytes + (KSA_LPR - 1) * 16u;
         asm volatile("" : "+s"(lim));
