@@ -59,6 +59,9 @@ def parse():
     ap.add_argument('--rotate', type=int, default=8, help='rotating buffer sets per launch')
     ap.add_argument('--eager', action='store_true', help='launch from Python instead of replaying HIP graphs')
     ap.add_argument('--cpu-sample-m', type=int, default=512)
+    ap.add_argument('--hipblaslt', action='store_true',
+                    help='dense workload: also time the vendor FP8 GEMM (torch._scaled_mm -> hipBLASLt) on the same '
+                         'shapes with per-tensor and row-wise scales, for context (not part of value)')
     ap.add_argument('--calibrate-copy-mib', type=int, default=0,
                     help='first run torch.neg over this many MiB of float32 (a plain copy kernel of known '
                          'size, the reference for FETCH_SIZE / WRITE_SIZE counter passes)')
@@ -67,6 +70,62 @@ def parse():
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def hipblaslt_context(rot: int, reps: int):
+    """The vendor library's FP8 GEMM on the dense shapes, timed as the headline is
+    (flush, then `rot` back-to-back launches on rotating operand sets): torch's
+    _scaled_mm (hipBLASLt on ROCm) with one per-tensor scale, and with row-wise
+    scales (per row of A, per column of B, applied once in the epilogue). Neither
+    has the per-128-K block scales of the path this library implements, so both
+    do less work per output; the numbers are context for the roofline fraction."""
+    import torch
+    dev = 'cuda:0'
+    stream = torch.cuda.current_stream()
+    flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+    m = 4096
+    for mode in ('per_tensor', 'row_wise'):
+        per, tot_us, tot_fl = {}, 0.0, 0
+        for n, k in DENSE_NK:
+            fns = []
+            for _ in range(rot):
+                a = torch.randn((m, k), device=dev, generator=gen).to(torch.float8_e4m3fn)
+                b = torch.randn((n, k), device=dev, generator=gen).to(torch.float8_e4m3fn)
+                if mode == 'per_tensor':
+                    sa, sb = torch.ones((), device=dev), torch.ones((), device=dev)
+                else:
+                    sa, sb = torch.ones((m, 1), device=dev), torch.ones((1, n), device=dev)
+                fns.append(lambda a=a, b=b, sa=sa, sb=sb: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb,
+                                                                          out_dtype=torch.bfloat16))
+            try:
+                for f in fns:
+                    f()
+                torch.cuda.synchronize()
+            except Exception as e:   # a torch build without this form: say so, time nothing
+                out[mode] = {'error': f'{type(e).__name__}: {str(e)[:160]}'}
+                break
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for e0, e1 in evs:
+                torch.sum(flush, dtype=torch.int64)
+                e0.record(stream)
+                for f in fns:
+                    f()
+                e1.record(stream)
+            torch.cuda.synchronize()
+            us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / (reps * rot)
+            per[f'n{n}_k{k}'] = round(us, 2)
+            tot_us += us
+            tot_fl += 2 * m * n * k
+            del fns
+            torch.cuda.empty_cache()
+        else:
+            out[mode] = {'per_launch_us': per, 'step_us': round(tot_us, 1),
+                         'tflops': round(tot_fl / tot_us / 1e6, 1),
+                         'frac': round(tot_fl / tot_us / 1e6 / PEAK_FP8_TFLOPS, 4)}
+    del flush
+    return out
 
 
 # ---------------------------------------------------------------- workloads
@@ -674,6 +733,9 @@ def main():
             del w
             torch.cuda.empty_cache()
         out['other_configs'] = extras
+    if args.workload == 'dense' and args.hipblaslt:
+        log('hipBLASLt context ...')
+        out['hipblaslt_fp8_context'] = hipblaslt_context(rot, reps)
     if not args.no_cpu_baseline:
         log('cpu baseline ...')
         out['cpu_baseline'] = cpu_baseline(args.workload, args.cpu_sample_m)
