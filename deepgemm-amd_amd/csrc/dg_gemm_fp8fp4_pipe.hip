@@ -309,6 +309,14 @@ fp8_fp4_gemm_pipe_kernel(const Fp8Fp4GemmArgs p, const int num_m_blocks, const i
                             opB[j][ks] = frag(next_stage + B_OFF, wn * WN + j * 32, ks, BTag{});
                     }
                 }
+                if (i + 1 < SM) {
+                    // one MFMA, then one LDS read of the next slice's fragments
+#pragma unroll
+                    for (int q = 0; q < 2 * SN; ++q) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    }
+                }
             }
         }
     }
