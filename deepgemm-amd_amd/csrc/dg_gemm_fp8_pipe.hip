@@ -579,6 +579,18 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                     }
                 }
             }
+            if constexpr (PIN_PROMO) {
+                // the slice's MFMAs alternate with the next slice's fragment reads
+                // (config-2 step 848-864 against 849-872 us, and 236 instead of
+                // 252 registers: the reads are no longer all hoisted)
+                if (i + 1 < SM) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    }
+                }
+            }
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e)
