@@ -348,9 +348,10 @@ int64_t dense_split_columns(int64_t m_rows, int64_t n, int64_t k, int cus) {
     const double whole = rounds(mb * ceil_div(n, 256)) * t256;
     double best = whole;
     int64_t best_n1 = 0;
+    // (on equal cost the largest n1: the most work in the 256 x 256 launch)
     for (int64_t n1 = 256; n1 < n; n1 += 256) {
         const double cost = rounds(mb * (n1 / 256)) * t256 + rounds(mb * ceil_div(n - n1, 192)) * t192;
-        if (cost < best - 1e-9) best = cost, best_n1 = n1;
+        if (cost < best - 1e-9 || (best_n1 > 0 && cost <= best + 1e-9)) best = cost, best_n1 = n1;
     }
     return best < 0.95 * whole ? best_n1 : 0;
 }

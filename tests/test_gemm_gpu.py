@@ -100,7 +100,8 @@ def test_all_tiles_bitwise_equal(m, n, k):
         assert torch.equal(o.view(torch.int16), outs[0][1].view(torch.int16))
 
 
-@pytest.mark.parametrize('m,n,k,acc', [(4096, 7168, 4096, False), (4096, 7168, 4096, True), (8192, 7168, 4096, False)])
+@pytest.mark.parametrize('m,n,k,acc', [(4096, 7168, 4096, False), (4096, 7168, 4096, True), (8192, 7168, 4096, False),
+                                        (4096, 7040, 4096, False)])   # the 256 x 192 launch ends in a 64-column tile
 def test_dense_column_split_equals_one_launch(m, n, k, acc):
     """Dense calls (K >= 4096) whose 256 x 256 tiles would leave the last round part
     empty run as two launches (256 x 256 tiles over the first columns, 256 x 192 over the rest):
