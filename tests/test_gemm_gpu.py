@@ -52,6 +52,7 @@ DENSE_CASES = [
     (300, 4096, 512),
     (7, 16, 16),         # K shorter than one block
     (256, 512, 1040),    # K tail (K % 128 == 16)
+    (512, 768, 36864),   # more K blocks than the 4-block SFA scale groups hold: per-stage SFA loads
 ]
 
 
