@@ -15,7 +15,9 @@ import os
 import torch
 
 _LIB_NAME = 'libdeepgemm_mi355x.so'
-_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+# DG_LIBRARY names another build of the same library (the sanitizer build of the
+# host layer, tests/sanitize/build_asan.sh); by default the in-tree library.
+_LIB_PATH = os.environ.get('DG_LIBRARY') or os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
 
 DG_OK, DG_ERR_INVALID, DG_ERR_UNSUPPORTED, DG_ERR_HIP, DG_ERR_INTERNAL = 0, 1, 2, 3, 4
 DG_F32, DG_BF16, DG_E4M3, DG_I32, DG_I8, DG_U8, DG_F16, DG_I64 = range(8)
