@@ -59,6 +59,9 @@ def parse():
     ap.add_argument('--rotate', type=int, default=8, help='rotating buffer sets per launch')
     ap.add_argument('--eager', action='store_true', help='launch from Python instead of replaying HIP graphs')
     ap.add_argument('--cpu-sample-m', type=int, default=512)
+    ap.add_argument('--hbm-context', action='store_true',
+                    help='masked workload: also time torch\'s own streaming read (sum) and copy over 1-4 GiB, '
+                         'for context on the HBM roofline (not part of value)')
     ap.add_argument('--hipblaslt', action='store_true',
                     help='dense workload: also time the vendor FP8 GEMM (torch._scaled_mm -> hipBLASLt) on the same '
                          'shapes with per-tensor and row-wise scales, for context (not part of value)')
@@ -70,6 +73,38 @@ def parse():
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def hbm_context(reps: int):
+    """HBM rates of torch's own kernels on this GPU, timed as the launches are (a
+    read flush, then one call between two events): a reduction (`sum`, read only)
+    and a device copy (read + write) over 1, 2 and 4 GiB of float32."""
+    import torch
+    dev = 'cuda:0'
+    stream = torch.cuda.current_stream()
+    flush = torch.ones(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    out = {}
+    for gib in (1, 2, 4):
+        n = gib * 2 ** 30 // 4
+        x = torch.randn(n, device=dev)
+        y = torch.empty_like(x)
+        x.sum()
+        y.copy_(x)
+        torch.cuda.synchronize()
+        for name, fn, nbytes in (('sum_read', lambda: x.sum(), 4 * n), ('copy_read_write', lambda: y.copy_(x), 8 * n)):
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for e0, e1 in evs:
+                torch.sum(flush, dtype=torch.int64)
+                e0.record(stream)
+                fn()
+                e1.record(stream)
+            torch.cuda.synchronize()
+            us = sum(e0.elapsed_time(e1) for e0, e1 in evs) * 1e3 / reps
+            out[f'{name}_{gib}gib_gbs'] = round(nbytes / us / 1e3, 1)
+        del x, y
+        torch.cuda.empty_cache()
+    del flush
+    return out
 
 
 def hipblaslt_context(rot: int, reps: int):
@@ -733,6 +768,9 @@ def main():
             del w
             torch.cuda.empty_cache()
         out['other_configs'] = extras
+    if args.workload == 'masked' and args.hbm_context:
+        log('HBM context ...')
+        out['hbm_context'] = hbm_context(reps)
     if args.workload == 'dense' and args.hipblaslt:
         log('hipBLASLt context ...')
         out['hipblaslt_fp8_context'] = hipblaslt_context(rot, reps)
