@@ -356,6 +356,38 @@ int64_t dense_split_columns(int64_t m_rows, int64_t n, int64_t k, int cus) {
     return best < 0.95 * whole ? best_n1 : 0;
 }
 
+// Row split of an m-grouped contiguous call (m_indices layout) whose 256 x 256
+// tiles leave the last round mostly empty (8 experts, 32768 tokens, N = 4096:
+// 131 M blocks x 16 = 2096 tiles, 8 full rounds and 48 tiles): rows [0, r1) run
+// as 256 x 256 tiles and rows [r1, M) as smaller tiles (there 192 tiles of
+// 128 x 128, each a quarter of the work). r1 is a multiple of 256 and segments
+// start on the M alignment, so each part is itself an m_indices layout; every
+// tile shape computes its outputs with the same arithmetic, so the result is
+// bitwise that of one launch. Returns r1 and the second launch's tile, or 0 when
+// the per-round cost model gains less than 5% or K is under 4096 (as for the
+// column split).
+int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int align_m, TileConfig& hi_tile) {
+    if (k < 4096) return 0;
+    struct Part { int bm, bn; double eff; };
+    static const Part parts[] = {{256, 128, 1.00}, {128, 256, 0.97}, {128, 128, 0.80}};   // as in choose_tile_1d2d
+    constexpr double t256 = 256.0 * 256 / 1.32;
+    const int64_t mb = ceil_div(m_rows, 256);
+    auto rounds = [&](int64_t tiles) { return (double)ceil_div(tiles, (int64_t)cus); };
+    const double whole = rounds(mb * ceil_div(n, 256)) * t256;
+    double best = whole;
+    int64_t best_r1 = 0;
+    // (on equal cost the largest r1: the most work in the 256 x 256 launch)
+    for (int64_t mb1 = mb - 1; mb1 >= 1; --mb1)
+        for (const auto& p : parts) {
+            if (!grouped_tile_ok(kContiguous, 2, p.bm, align_m)) continue;
+            const int64_t rows2 = m_rows - mb1 * 256;
+            const double cost = rounds(mb1 * ceil_div(n, 256)) * t256 +
+                                rounds(ceil_div(rows2, p.bm) * ceil_div(n, p.bn)) * (p.bm * p.bn / p.eff);
+            if (cost < best - 1e-9) best = cost, best_r1 = mb1 * 256, hi_tile = TileConfig{p.bm, p.bn, 2};
+        }
+    return best < 0.95 * whole ? best_r1 : 0;
+}
+
 void record_config(const char* kernel, GemmKind kind, const TileConfig& t, int64_t m, int64_t n, int64_t k,
                    int64_t g) {
     char buf[256];
@@ -518,6 +550,29 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
                 hi.d = static_cast<uint8_t*>(args.d) + n1 * elem;
                 if (args.c) hi.c = static_cast<const uint8_t*>(args.c) + n1 * elem;
                 launch_fp8_gemm_1d2d_v2(kind, TileConfig{256, 192, 2}, hi, stream);
+                return;
+            }
+        }
+        if (kind == kContiguous && tv == 0 && t.variant == 2 && t.block_m == 256 && t.block_n == 256) {
+            TileConfig ht{};
+            const int64_t r1 = contiguous_split_rows(m_rows, n, k, args.grid_limit, align_m, ht);
+            if (r1 > 0) {
+                t_last_config += " split_m=" + std::to_string(r1) + ":" + std::to_string(ht.block_m) + "x" +
+                                 std::to_string(ht.block_n);
+                Fp8GemmArgs lo = args;
+                lo.m = (int32_t)r1;
+                launch_fp8_gemm_1d2d_v2(kind, t, lo, stream);
+                // rows [r1, m): A rows, SFA rows (K- or MN-major: sfa_sm is the row
+                // stride), m_indices entries and D rows
+                Fp8GemmArgs hi = args;
+                hi.m = (int32_t)(m_rows - r1);
+                hi.a = args.a + r1 * args.lda;
+                hi.sfa = args.sfa + r1 * args.sfa_sm;
+                hi.layout = args.layout + r1;
+                const int64_t elem = args.out_f32 ? 4 : 2;
+                hi.d = static_cast<uint8_t*>(args.d) + r1 * args.ldd * elem;
+                if (args.c) hi.c = static_cast<const uint8_t*>(args.c) + r1 * args.ldc * elem;
+                launch_fp8_gemm_1d2d_v2(kind, ht, hi, stream);
                 return;
             }
         }

@@ -72,8 +72,9 @@ def phase_slices(num_launches: int, steps: int, rot: int, disp=None):
 
 
 def dispatches_per_call(config: str) -> int:
-    """Kernels one library call dispatches: a dense column split runs two."""
-    return 2 if 'split_n=' in config else 1
+    """Kernels one library call dispatches: a dense column split or a contiguous
+    row split runs two."""
+    return 2 if ('split_n=' in config or 'split_m=' in config) else 1
 
 
 def read_trace(path):

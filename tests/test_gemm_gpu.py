@@ -296,6 +296,72 @@ def _contiguous_case(ms, aligned, n, k):
     assert torch.equal(d.view(torch.int16), first.view(torch.int16))
 
 
+@pytest.mark.parametrize('ms,mn_major', [(None, False), ([8000, 0, 16500, 8700], True)])
+def test_contiguous_row_split_equals_one_launch(ms, mn_major):
+    """m-grouped contiguous calls (K >= 4096) whose 256 x 256 tiles would leave the
+    last round mostly empty run as two launches (the first rows on 256 x 256 tiles,
+    the last M blocks on smaller ones): bitwise the single 256 x 256 launch, padding
+    rows untouched, and rows on both sides of the split against the oracle. Cases:
+    config 3's token count (8 experts, Dirichlet sizes, 131 M blocks) and a split
+    inside a segment after an empty expert, with MN-major SFA."""
+    n, k = 4096, 4096
+    if ms is None:
+        ms, aligned = gen.contiguous_sizes(8, 32768, seed=7)
+    else:
+        aligned = [(x + 127) // 128 * 128 for x in ms]
+    g, m_pad = len(ms), sum(aligned)
+    print(f'contiguous row split ms={ms} m_pad={m_pad} mn_major={mn_major}', flush=True)
+    dg = torch.Generator(device=DEV).manual_seed(41)
+    a_bf = torch.randn((m_pad, k), generator=dg, device=DEV).bfloat16()
+    layout_np = np.full(m_pad, -1, dtype=np.int32)
+    start = 0
+    for e, (mi, ai) in enumerate(zip(ms, aligned)):
+        layout_np[start:start + mi] = e
+        a_bf[start + mi:start + ai] = 0   # padding rows of A are zero, as the reference's generator writes them
+        start += ai
+    layout = gen.to_dev(layout_np)
+    aq, asf = deep_gemm.per_token_cast_to_fp8(a_bf, use_ue8m0=False)
+    if mn_major:
+        asf = deep_gemm.get_mn_major_tma_aligned_tensor(asf)
+    bq = torch.empty((g, n, k), dtype=torch.float8_e4m3fn, device=DEV)
+    bs = torch.empty((g, n // 128, k // 128), device=DEV)
+    for e in range(g):
+        bq[e], bs[e] = deep_gemm.per_block_cast_to_fp8(torch.randn((n, k), generator=dg, device=DEV).bfloat16(),
+                                                       use_ue8m0=False)
+
+    def run():
+        d = sentinel_bf16((m_pad, n))
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous((aq, asf), (bq, bs), d, layout)
+        return d, deep_gemm.get_last_config()
+
+    split, cfg = run()
+    print(cfg, flush=True)
+    assert 'split_m=' in cfg, cfg
+    try:
+        deep_gemm.set_tile_override(256, 256, variant=2)
+        whole, cfg1 = run()
+        assert 'split_m=' not in cfg1, cfg1
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(split.view(torch.int16), whole.view(torch.int16))
+    valid = torch.from_numpy(layout_np >= 0).to(DEV)
+    assert bool((split.view(torch.int16)[~valid] == SENTINEL).all()), 'padding rows touched'
+    # rows on both sides of the split row, and the first and last valid rows, against the oracle
+    r1 = int(cfg.split('split_m=')[1].split(':')[0])
+    cand = [0, r1 - 2, r1 - 1, r1, r1 + 1, int(np.nonzero(layout_np >= 0)[0][-1])]
+    rows = np.array(sorted({r for r in cand if 0 <= r < m_pad and layout_np[r] >= 0}))
+    a_deq = oquant.dequant_per_token(aq[rows].view(torch.uint8).cpu().numpy(), asf[rows].cpu().numpy())
+    out = split[torch.from_numpy(rows).to(DEV)].float().cpu().numpy()
+    ref = np.empty_like(out, dtype=np.float64)
+    for e in np.unique(layout_np[rows]):
+        sel = layout_np[rows] == e
+        b_deq = oquant.dequant_per_block(bq[e].view(torch.uint8).cpu().numpy(), bs[e].cpu().numpy())
+        ref[sel] = ogemm.gemm_nt(a_deq[sel], b_deq)
+    diff, _ = report('contiguous row split', out, ref)
+    assert diff < 1e-5
+
+
 def test_psum_layout():
     """psum layout against the oracle's restatement of the reference's psum walk
     (oracle/gemm.py psum_blocks / gemm_psum): computed rows match the FP64

@@ -75,3 +75,10 @@ def test_split_launch_calls_span_both_dispatches(tmp_path):
     assert out['per_launch_bytes']['n7168_k16384']['write'] == 200 * 1024
     md = (tmp_path / 'out.md').read_text()
     assert '| 256+256 |' in md and '| 10 |' in md   # grids of both dispatches; 10 calls in the phase
+
+
+def test_dispatches_per_call():
+    assert rs.dispatches_per_call('fp8_gemm_1d2d v2 kind=normal block_m=256 block_n=256') == 1
+    assert rs.dispatches_per_call('fp8_gemm_1d2d v2 kind=normal block_m=256 block_n=256 split_n=4096:256x192') == 2
+    assert rs.dispatches_per_call('fp8_gemm_1d2d v2 kind=m_grouped_contiguous block_m=256 block_n=256 '
+                                  'split_m=32768:128x128') == 2
