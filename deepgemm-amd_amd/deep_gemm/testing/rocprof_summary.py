@@ -122,13 +122,14 @@ def summarize(args):
     per = []
     for name, sl, d in zip(names, slices, disp):
         rows = [seq[i][2] for i in sl]
-        kern = {_short(r['Kernel_Name']) for r in rows}
+        # kernel names in dispatch order (a split call runs two different tiles)
+        kern = dict.fromkeys(_short(rows[j]['Kernel_Name']) for j in range(d))
         # one call = d consecutive dispatches: first start to last end
         durs = [(int(rows[c + d - 1]['End_Timestamp']) - int(rows[c]['Start_Timestamp'])) / 1e3
                 for c in range(0, len(rows), d)]
         r0 = rows[0]
         grids = [int(rows[j]['Grid_Size_X']) // max(1, int(rows[j]['Workgroup_Size_X'])) for j in range(d)]
-        per.append({'launch': name, 'kernel': ' / '.join(sorted(kern)), 'calls': len(durs),
+        per.append({'launch': name, 'kernel': ' / '.join(kern), 'calls': len(durs),
                     'avg_us': sum(durs) / len(durs), 'min_us': min(durs), 'max_us': max(durs),
                     'event_us': roof['per_launch_us'][name],
                     'grid': grids[0] if d == 1 else '+'.join(str(g) for g in grids),
