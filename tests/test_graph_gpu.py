@@ -111,3 +111,37 @@ def test_graph_cast():
         torch.cuda.synchronize()
         assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
         assert torch.equal(sf.view(torch.int32), sf0.view(torch.int32))
+
+
+def test_graph_split_calls():
+    """Calls that run as two launches (a dense column split, a contiguous row
+    split) capture as both kernels and replay bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(9)
+    m, n, k = 4096, 7168, 4096
+    a = deep_gemm.per_token_cast_to_fp8(torch.randn((m, k), generator=g, device=DEV).bfloat16(), use_ue8m0=False)
+    b = deep_gemm.per_block_cast_to_fp8(torch.randn((n, k), generator=g, device=DEV).bfloat16(), use_ue8m0=False)
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    print('graph dense split 4096x7168x4096', flush=True)
+    replay_matches_eager(lambda: deep_gemm.fp8_gemm_nt(a, b, d), d)
+    assert 'split_n=' in deep_gemm.get_last_config()
+
+    ms, aligned = gen.contiguous_sizes(8, 32768, seed=7)   # 33408 rows: 131 M blocks
+    n, k = 4096, 4096
+    m_pad = sum(aligned)
+    layout_np = np.full(m_pad, -1, dtype=np.int32)
+    start = 0
+    for e, (mi, ai) in enumerate(zip(ms, aligned)):
+        layout_np[start:start + mi] = e
+        start += ai
+    layout = gen.to_dev(layout_np)
+    ca = deep_gemm.per_token_cast_to_fp8(torch.randn((m_pad, k), generator=g, device=DEV).bfloat16(), use_ue8m0=False)
+    bq = torch.empty((8, n, k), dtype=torch.float8_e4m3fn, device=DEV)
+    bs = torch.empty((8, n // 128, k // 128), device=DEV)
+    for e in range(8):
+        bq[e], bs[e] = deep_gemm.per_block_cast_to_fp8(torch.randn((n, k), generator=g, device=DEV).bfloat16(),
+                                                       use_ue8m0=False)
+    dc = torch.empty((m_pad, n), dtype=torch.bfloat16, device=DEV)
+    print(f'graph contiguous split m_pad={m_pad}', flush=True)
+    replay_matches_eager(lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(ca, (bq, bs), dc, layout), dc,
+                         written=torch.from_numpy(layout_np >= 0).to(DEV))
+    assert 'split_m=' in deep_gemm.get_last_config()
