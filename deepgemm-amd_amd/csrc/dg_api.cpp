@@ -38,14 +38,29 @@ constexpr int kDenseStreamRows = 64;
 // even at 7168 x 2048 with 64 rows.
 constexpr int kTinyMStreamGrid = 64;
 
-// Tiny-M configuration (measured): 8 waves when the rows are few, K is long
-// (each wave gets at least 6 K blocks) and the workgroups are narrow, else 4
-// (fewer workgroup-wide A re-reads per K block); 32 columns per workgroup once
-// N / 16 exceeds the CU count, else 16.
-TileConfig choose_tinym(int64_t m, int64_t n, int64_t k) {
-    const int waves_variant = (m <= 16 && k / 128 >= 48 && n <= 4096) ? 8 : 9;
-    const int cols = n > 4096 ? 32 : 16;
-    return TileConfig{kTinyMRows, cols, waves_variant};
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// The tiny-M kernel's workgroup shape: rows (16, 32 or 64) x columns (16 or 32).
+// A workgroup reads (rows + columns) x K bytes (A's rows once, all of K, and its
+// B rows), and the launch runs ceil(workgroups / CUs) rounds of them; the model
+// takes the fewest bytes per CU, and on equal cost more columns. Measured
+// (flushed, per launch): 64 x 2112 x 7168 29.3 -> 23.9 us (32 x 32 against
+// 64 x 16), 64 x 576 x 7168 29.0 -> 14.7, 64 x 4096 x 4096 20.9 -> 15.0; the
+// N = 7168 shapes keep 64-row workgroups. 8 waves pay with 16 columns, 16 rows
+// and long K (at 32 columns they are slower: 21.6 against 18.1 us at
+// 32 x 2112 x 7168).
+TileConfig choose_tinym(int64_t m, int64_t n, int64_t k, int cus) {
+    const int64_t m16 = ceil_div(m, 16) * 16;
+    int best_rows = kTinyMRows, best_cols = 16;
+    int64_t best = INT64_MAX;
+    for (int cols : {32, 16})
+        for (int rows : {64, 32, 16}) {
+            const int64_t wgs = ceil_div(n, (int64_t)cols) * ceil_div(m, (int64_t)rows);
+            const int64_t cost = ceil_div(wgs, (int64_t)cus) * (std::min<int64_t>(rows, m16) + cols);
+            if (cost < best) best = cost, best_rows = rows, best_cols = cols;
+        }
+    const bool eight = std::min<int64_t>(best_rows, m16) <= 16 && k / 128 >= 48 && best_cols == 16;
+    return TileConfig{best_rows, best_cols, eight ? 8 : 9};
 }
 std::atomic<int> g_num_sms{0};                 // 0: query the device
 std::atomic<int> g_mk_alignment{kDefaultMKAlignment};
@@ -69,7 +84,6 @@ int guarded(F&& f) {
     }
 }
 
-int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
 int elem_size(int dtype) {
@@ -509,12 +523,12 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
             if (!tinym_ok)
                 DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 64 rows with "
                                "K % 128 == 0, K <= 32768, BF16 D and no C");
-            t = {kTinyMRows, g_tile_n.load(), tv};
+            t = {g_tile_m.load(), g_tile_n.load(), tv};   // rows per workgroup, columns per workgroup
         } else if (tv == 0 && tinym_ok &&
                    (!stream_ok || (n + 32 * fp8_masked_stream_waves(n, 1, args.grid_limit) - 1) /
                                           (32 * fp8_masked_stream_waves(n, 1, args.grid_limit)) <
                                       kTinyMStreamGrid)) {
-            t = choose_tinym(m_rows, n, k);
+            t = choose_tinym(m_rows, n, k, args.grid_limit);
         } else if (tv == 5) {   // forced: the weight-streaming kernel
             if (!stream_ok)
                 DG_UNSUPPORTED("tile override: the weight-streaming kernel runs the masked layout, or dense calls of at "
@@ -577,7 +591,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
             }
         }
         if (t.variant == 8 || t.variant == 9)
-            launch_fp8_gemm_tinym(args, t.variant == 8 ? 8 : 4, t.block_n, stream);
+            launch_fp8_gemm_tinym(args, t.variant == 8 ? 8 : 4, t.block_n, t.block_m, stream);
         else if (t.variant == 5)
             launch_fp8_gemm_masked_stream(args, t.block_n / 32, t.block_m == kStream16Rows, stream);
         else if (t.variant >= 2)
@@ -1334,7 +1348,8 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
                         : variant == 6 ? (block_m == 128 && (block_n == 128 || block_n == 192 || block_n == 256))
                         : variant == 7 ? (block_m == 128 && block_n == 128)
                         : variant == 8 || variant == 9
-                            ? (block_m == kTinyMRows && (block_n == 16 || block_n == 32 || block_n == 64))
+                            ? ((block_m == 16 || block_m == 32 || block_m == kTinyMRows) &&
+                               (block_n == 16 || block_n == 32 || block_n == 64))
                                        : (variant == 4 && block_m == 256 && block_n == 256);
         if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;

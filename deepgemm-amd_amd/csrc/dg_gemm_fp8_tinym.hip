@@ -15,8 +15,11 @@
 //    4 (l >> 4) + e of token l & 15) and promotes it, fin = fma(sa * sb, acc,
 //    fin); with RT row tiles of 16 (M <= 16 RT), each K block also loads RT A
 //    fragments and issues RT x CG MFMAs. Since the waves split K, every
-//    workgroup reads all of A (from L2): N / (16 CG) times A's bytes, which is
-//    why CG > 1 pays at large N and M;
+//    workgroup reads all of its rows of A (from L2): N / (16 CG) times A's
+//    bytes, which is why CG > 1 pays at large N and M;
+//  * the rows may be split over workgroups too (16 RT rows each, the grid's
+//    y dimension): more workgroups, each reading a slice of A. A row tile's
+//    arithmetic does not depend on RT, so every split gives the same bits;
 //  * the fragments come straight from global memory into registers (a lane's
 //    32 bytes are contiguous in its row), kept 2 to 8 blocks ahead in a
 //    register ring; no LDS, no barrier in the K loop; the B scales of a wave's
@@ -24,7 +27,8 @@
 //  * the NW partial sums meet in LDS and wave 0 adds them in wave order, so the
 //    result is deterministic (no atomics, no workspace); then one rounding to
 //    BF16.
-// So a launch has N / (16 CG) workgroups of NW waves, several per CU. The sums are
+// So a launch has N / (16 CG) x ceil(M / 16 RT) workgroups of NW waves, several
+// per CU. The sums are
 // grouped differently from the single-pass kernels (per wave, then across
 // waves), so the bits differ from theirs; it is its own configuration
 // (variant 8).
@@ -68,6 +72,7 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * (16 * CG);
+    const int m0 = blockIdx.y * (16 * RT);   // the workgroup's first row
     const int r = lane & 15, q = lane >> 4;
     const int num_kb = p.k / kBK;
 
@@ -79,7 +84,7 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
     const float* __restrict__ sa_row[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
-        const int m = min(16 * t + r, p.m - 1);
+        const int m = min(m0 + 16 * t + r, p.m - 1);
         a_row[t] = p.a + (int64_t)m * p.lda + 32 * q;
         sa_row[t] = p.sfa + (int64_t)m * p.sfa_sm;
     }
@@ -185,8 +190,8 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = v[e] + u[e];
         }
-        // lane l: token 16 t + (l & 15), columns n0 + 16 c + 4 (l >> 4) + (0..3)
-        const int row = 16 * t + r;
+        // lane l: token m0 + 16 t + (l & 15), columns n0 + 16 c + 4 (l >> 4) + (0..3)
+        const int row = m0 + 16 * t + r;
         const int col = n0 + 16 * c + 4 * q;
         if (row < p.m && col < p.n) {
             uint16_t* dp = static_cast<uint16_t*>(p.d) + (int64_t)row * p.ldd + col;
@@ -212,8 +217,10 @@ bool fp8_tinym_supported(const Fp8GemmArgs& a) {
 template <int NW, int RT, int CG>
 void launch_cfg(const Fp8GemmArgs& a, hipStream_t stream) {
     const int64_t grid = (a.n + 16 * CG - 1) / (16 * CG);
-    DG_CHECK(grid < (int64_t)1 << 31);
-    hipLaunchKernelGGL((fp8_gemm_tinym_kernel<NW, RT, CG>), dim3((unsigned)grid), dim3(NW * 64), 0, stream, a);
+    const int64_t row_groups = (a.m + 16 * RT - 1) / (16 * RT);   // workgroups of 16 RT rows each
+    DG_CHECK(grid < (int64_t)1 << 31 && row_groups <= 4);
+    hipLaunchKernelGGL((fp8_gemm_tinym_kernel<NW, RT, CG>), dim3((unsigned)grid, (unsigned)row_groups), dim3(NW * 64),
+                       0, stream, a);
 }
 
 template <int RT>
@@ -230,9 +237,12 @@ void launch_rt(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream) {
     }
 }
 
-void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream) {
+void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, int rows, hipStream_t stream) {
     DG_CHECK(fp8_tinym_supported(a));
-    switch ((a.m + 15) / 16) {
+    DG_CHECK(rows == 16 || rows == 32 || rows == 64);
+    // row tiles per workgroup: the rows that exist, at most rows / 16
+    const int tiles = (a.m + 15) / 16;
+    switch (tiles < rows / 16 ? tiles : rows / 16) {
         case 1: launch_rt<1>(a, waves, cols, stream); break;
         case 2: launch_rt<2>(a, waves, cols, stream); break;
         case 3: launch_rt<3>(a, waves, cols, stream); break;

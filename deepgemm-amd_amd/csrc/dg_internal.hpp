@@ -95,7 +95,7 @@ struct TileConfig {
 // (dg_gemm_fp8_tinym.hip): M <= 64, K % 128 == 0, BF16 D, no C.
 constexpr int kTinyMRows = 64;
 bool fp8_tinym_supported(const Fp8GemmArgs& a);
-void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, hipStream_t stream);
+void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, int rows, hipStream_t stream);
 
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
 // Throws dgm::Error on unsupported configurations or launch failures.

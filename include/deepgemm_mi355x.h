@@ -358,7 +358,10 @@ int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m
  * set_block_size_multiple_of, csrc/apis/config.hpp:40-47). variant 1 = the
  * register-staged kernel, 2 = the LDS-pipelined kernel (both 32x32x64 MFMA),
  * 4 = the pipelined kernel with persistent workgroups (one per CU, striding
- * over the tile sequence like the reference's scheduler; 256 x 256 only);
+ * over the tile sequence like the reference's scheduler; 256 x 256 only),
+ * 5 = the weight-streaming kernel (block_m 16 or 160 rows per pass), 6 / 7 =
+ * the 1D1D kernels, 8 / 9 = the tiny-M kernel with 8 / 4 waves (block_m = rows
+ * per workgroup, 16, 32 or 64; block_n = columns per workgroup, 16, 32 or 64);
  * variant 0 restores the heuristic. Only compiled tile shapes are accepted. */
 int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n);
 

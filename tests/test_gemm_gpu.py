@@ -571,22 +571,26 @@ def test_dense_tiny_m_on_stream_kernel(m):
                                    (64, 2112, 7168), (50, 104, 1024), (17, 4096, 4096), (3, 104, 32768)])
 def test_dense_tiny_m_split_k_kernel(m, n, k):
     """The tiny-M kernel (K split over the waves of a workgroup, partial sums
-    added in wave order; up to four 16-row tiles), in each of its configurations
-    (8 or 4 waves; 16, 32 or 64 columns per workgroup, 64 up to 32 rows): the
-    oracle within one BF16 ulp plus the FP32 accumulation bound, ragged M and N
-    (104, not a multiple of 16 or 32), fewer K blocks than waves (K = 128, 384),
-    the largest K (256 blocks: 64 per wave at 4 waves), MN-major SFA equal to
-    K-major, and bitwise-identical reruns. The default routing takes it for N
-    up to 7168; config 1 of the benchmark (64 x 2112 x 7168) is one of these."""
+    added in wave order; up to four 16-row tiles per workgroup), in each of its
+    configurations (8 or 4 waves; 16, 32 or 64 columns and 16, 32 or 64 rows per
+    workgroup, 64 columns up to 32 rows): the oracle within one BF16 ulp plus
+    2^-15 x sum |a b|, ragged M and N (104, not a multiple of 16 or 32), fewer K
+    blocks than waves (K = 128, 384), the largest K (256 blocks: 64 per wave at 4
+    waves), MN-major SFA equal to K-major, bitwise-identical reruns, and the same
+    bits for every split of the rows over workgroups. The default routing takes
+    it for N up to 7168; config 1 of the benchmark (64 x 2112 x 7168) is one of these."""
     x = gen.dense_inputs(m, n, k, seed=90 + m + n)
-    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    a_deq, b_deq = oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb'])
+    ref = ogemm.gemm_nt(a_deq, b_deq)
+    s_abs = ogemm.gemm_nt(np.abs(a_deq), np.abs(b_deq))
     a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
     sfa_mn = deep_gemm.get_mn_major_tma_aligned_tensor(a[1])
-    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(ref).max()
-    for v, bn in ((8, 16), (9, 16), (8, 32), (9, 32), (8, 64), (9, 64), (0, 0)):
-        if bn == 64 and m > 32:
+    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -15 * s_abs
+    by_cfg = {}
+    for v, bn, rows in [(v, bn, rows) for v in (8, 9) for bn in (16, 32, 64) for rows in (64, 32, 16)] + [(0, 0, 0)]:
+        if bn == 64 and rows > 32 and m > 32:
             continue
-        deep_gemm.set_tile_override(64 if v else 0, bn, variant=v)
+        deep_gemm.set_tile_override(rows, bn, variant=v)
         try:
             d = sentinel_bf16((m, n))
             deep_gemm.fp8_gemm_nt(a, b, d)
@@ -600,14 +604,17 @@ def test_dense_tiny_m_split_k_kernel(m, n, k):
         torch.cuda.synchronize()
         print(f'  {cfg}', flush=True)
         if v:
-            assert f' v{v} ' in cfg and f'block_n={bn} ' in cfg, cfg
+            assert f' v{v} ' in cfg and f'block_m={rows} block_n={bn} ' in cfg, cfg
         elif n <= 7168:
             assert ' v8 ' in cfg or ' v9 ' in cfg, cfg
         out = d.float().cpu().numpy()
-        diff, _ = report(f'dense tiny M={m} N={n} K={k} [{cfg.split(" kind")[0]} {bn}]', out, ref)
+        diff, _ = report(f'dense tiny M={m} N={n} K={k} [{cfg.split(" kind")[0]} {rows}x{bn}]', out, ref)
         assert diff < 1e-3
         assert np.all(np.abs(out - ref) <= tol)
         assert torch.equal(d2.view(torch.int16), d.view(torch.int16))
+        if v:   # a row tile's arithmetic does not depend on how the rows are split
+            first = by_cfg.setdefault((v, bn), d)
+            assert torch.equal(first.view(torch.int16), d.view(torch.int16)), f'rows {rows} differ'
 
 
 def test_dense_tiny_m_k_bound():
