@@ -77,6 +77,17 @@ def dispatches_per_call(config: str) -> int:
     return 2 if ('split_n=' in config or 'split_m=' in config) else 1
 
 
+def _workgroups(row) -> int:
+    """Workgroups of one dispatch: grid over workgroup size in each dimension the
+    trace has (Grid_Size_* counts work-items)."""
+    n = 1
+    for ax in 'XYZ':
+        g, w = row.get(f'Grid_Size_{ax}'), row.get(f'Workgroup_Size_{ax}')
+        if g not in (None, '') and w not in (None, ''):
+            n *= max(1, int(g) // max(1, int(w)))
+    return n
+
+
 def read_trace(path):
     rows = list(csv.DictReader(open(path)))
     rows.sort(key=lambda r: int(r['Dispatch_Id']))
@@ -128,7 +139,7 @@ def summarize(args):
         durs = [(int(rows[c + d - 1]['End_Timestamp']) - int(rows[c]['Start_Timestamp'])) / 1e3
                 for c in range(0, len(rows), d)]
         r0 = rows[0]
-        grids = [int(rows[j]['Grid_Size_X']) // max(1, int(rows[j]['Workgroup_Size_X'])) for j in range(d)]
+        grids = [_workgroups(rows[j]) for j in range(d)]
         per.append({'launch': name, 'kernel': ' / '.join(kern), 'calls': len(durs),
                     'avg_us': sum(durs) / len(durs), 'min_us': min(durs), 'max_us': max(durs),
                     'event_us': roof['per_launch_us'][name],
