@@ -30,12 +30,17 @@ constexpr int kDefaultMKAlignment = 128;
 // (measured on MI355X over the DeepSeek-V3 (N, K) shapes: faster than every
 // tiled configuration up to 64 rows, slower from 128).
 constexpr int kDenseStreamRows = 64;
-// Dense calls of at most 64 rows take the tiny-M kernel (K split over a
-// workgroup's waves, N / 16 or N / 32 workgroups) unless the streaming kernel
+// Dense calls of at most 64 rows, and of at most 128 rows with K <= 8192, take the
+// tiny-M kernel (K split over a workgroup's waves, rows split over workgroups)
+// unless the streaming kernel
 // already has this many workgroups (N >= 8192 or so), or the call has more than
 // 32 rows and fewer than 32 K blocks. Measured on MI355X at M = 1, 16, 17, 32
 // and 64: 1.2-2.6x faster for N <= 7168, slower at N = 24576 and 32768 and
-// even at 7168 x 2048 with 64 rows.
+// even at 7168 x 2048 with 64 rows. At 80-128 rows (flushed, per launch) it
+// takes 24-31 us against 46-51 us for the best tiled launch at 2112 x 7168,
+// 14-18 against 45-51 at 576 x 7168 and 21 against 30-34 at 4096 x 4096, ties
+// at 7168 x 2048, and loses at K = 16384 (97-120 against 93-102 us).
+constexpr int64_t kTinyMWideMaxK = 8192;
 constexpr int kTinyMStreamGrid = 64;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -515,13 +520,14 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         // the rows that exist (16 x 16 x 128 MFMAs up to 16 rows).
         const bool stream_ok = fp8_masked_stream_supported(args) &&
                                (kind == kMasked || (kind == kNormal && m_rows <= kMaskedStreamRows));
-        // Dense calls of at most 64 rows: K split over the waves of a workgroup, so
-        // the launch has N / 16 or N / 32 workgroups instead of the streaming
-        // kernel's N / 128.
-        const bool tinym_ok = kind == kNormal && fp8_tinym_supported(args);
+        // Dense calls of at most 64 rows (128 with K <= 8192): K split over the
+        // waves of a workgroup, so the launch has N / 16 or N / 32 workgroups per
+        // row group instead of the streaming kernel's N / 128.
+        const bool tinym_ok = kind == kNormal && fp8_tinym_supported(args) &&
+                              (tv == 8 || tv == 9 || m_rows <= kTinyMRows || k <= kTinyMWideMaxK);
         if (tv == 8 || tv == 9) {   // forced: the tiny-M kernel
             if (!tinym_ok)
-                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 64 rows with "
+                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 128 rows with "
                                "K % 128 == 0, K <= 32768, BF16 D and no C");
             t = {g_tile_m.load(), g_tile_n.load(), tv};   // rows per workgroup, columns per workgroup
         } else if (tv == 0 && tinym_ok &&

@@ -1,9 +1,9 @@
-// Dense FP32-scale FP8 GEMM for at most 64 rows of A (gfx950): decode-sized
+// Dense FP32-scale FP8 GEMM for at most 128 rows of A (gfx950): decode-sized
 // fp8_gemm_nt calls, D[m, n] = sum_k A[m, k] B[n, k] with the per-128-K FP32
 // promotion of the reference's 1D2D kernel
 // (deep_gemm/include/deep_gemm/impls/sm90_fp8_gemm_1d2d.cuh:281-345).
 //
-// At M <= 64 the call is a weight stream: N x K bytes of B against M x K of A.
+// At small M the call is a weight stream: N x K bytes of B against M x K of A.
 // The streaming kernel gives each workgroup 32 columns per wave and all of K,
 // so a launch has only N / 128 .. N / 256 workgroups (17 for N = 2112) and most
 // CUs stay idle. Here a workgroup owns 16 columns and splits K over its waves
@@ -32,7 +32,7 @@
 // grouped differently from the single-pass kernels (per wave, then across
 // waves), so the bits differ from theirs; it is its own configuration
 // (variant 8).
-// Requirements (checked by the host): M <= 64, K a multiple of 128 and at most
+// Requirements (checked by the host): M <= 128, K a multiple of 128 and at most
 // 32768, BF16 D without C, 16-byte aligned A and B rows.
 #include <hip/hip_runtime.h>
 
@@ -45,7 +45,7 @@ namespace {
 using namespace dev;
 
 constexpr int kBK = 128;
-constexpr int kRows = 64;
+constexpr int kMaxRows = 128;   // M; a workgroup takes at most 64 of the rows
 constexpr int kMaxKBlocks = 64 * 4;   // a wave's B scales fit one register: 64 blocks of 4 waves
 
 template <int RT, int CG>
@@ -209,7 +209,7 @@ fp8_gemm_tinym_kernel(const Fp8GemmArgs p) {
 }  // namespace
 
 bool fp8_tinym_supported(const Fp8GemmArgs& a) {
-    return a.m > 0 && a.m <= kRows && a.n > 0 && a.k > 0 && a.k % kBK == 0 && a.k / kBK <= kMaxKBlocks &&
+    return a.m > 0 && a.m <= kMaxRows && a.n > 0 && a.k > 0 && a.k % kBK == 0 && a.k / kBK <= kMaxKBlocks &&
            !a.out_f32 && a.c == nullptr &&
            a.num_groups == 1 && a.layout == nullptr;
 }
@@ -218,7 +218,7 @@ template <int NW, int RT, int CG>
 void launch_cfg(const Fp8GemmArgs& a, hipStream_t stream) {
     const int64_t grid = (a.n + 16 * CG - 1) / (16 * CG);
     const int64_t row_groups = (a.m + 16 * RT - 1) / (16 * RT);   // workgroups of 16 RT rows each
-    DG_CHECK(grid < (int64_t)1 << 31 && row_groups <= 4);
+    DG_CHECK(grid < (int64_t)1 << 31 && row_groups <= 8);
     hipLaunchKernelGGL((fp8_gemm_tinym_kernel<NW, RT, CG>), dim3((unsigned)grid, (unsigned)row_groups), dim3(NW * 64),
                        0, stream, a);
 }

@@ -91,8 +91,9 @@ struct TileConfig {
     int variant = 1;
 };
 
-// Dense calls of at most 64 rows with K split over the waves of a workgroup
-// (dg_gemm_fp8_tinym.hip): M <= 64, K % 128 == 0, BF16 D, no C.
+// Dense calls of at most 128 rows with K split over the waves of a workgroup
+// (dg_gemm_fp8_tinym.hip): M <= 128, K % 128 == 0, BF16 D, no C; a workgroup
+// takes at most kTinyMRows of the rows.
 constexpr int kTinyMRows = 64;
 bool fp8_tinym_supported(const Fp8GemmArgs& a);
 void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, int rows, hipStream_t stream);
