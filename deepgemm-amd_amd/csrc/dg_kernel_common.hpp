@@ -95,10 +95,21 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
                                             uint16_t* zero_d, int64_t ldd, int* s_flag, int raster_gm = 0) {
     Tile t{};
     int tile = xcd_remap(blockIdx.x, gridDim.x);
-    if constexpr (KIND == kMasked || KIND == kKGrouped) {
+    if constexpr (KIND == kMasked) {
         const int per_group = num_m_blocks * num_n_blocks;
         t.g = tile / per_group;
         tile -= t.g * per_group;
+    } else if constexpr (KIND == kKGrouped) {
+        // Chunks of C = per_group / 8 tiles cycle through the groups, so each XCD's
+        // contiguous range of tiles holds one chunk of every group (group-major,
+        // with 8 groups on 8 XCDs, each XCD would own one group and the XCD with
+        // the longest K_g would set the launch time), while a chunk keeps a
+        // group's neighbouring tiles together in one L2.
+        const int per_group = num_m_blocks * num_n_blocks;
+        const int c = per_group % 8 == 0 ? per_group / 8 : per_group;
+        const int q = tile / c;
+        t.g = q % num_groups;
+        tile = (q / num_groups) * c + (tile - q * c);
     }
     int mb, nb;
     raster_tile(tile, num_m_blocks, num_n_blocks, raster_gm, mb, nb);

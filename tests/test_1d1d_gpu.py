@@ -195,3 +195,36 @@ def test_1d1d_kernels_bitwise_equal(kg):
         outs.append(d)
     for o in outs[1:]:
         assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32))
+
+
+def test_k_grouped_chunked_group_order():
+    """Eight groups whose tile count (8 x 6 = 48 tiles of 128 x 128) is a multiple of
+    8: the launch walks the groups in chunks of 6 tiles, so each XCD holds a chunk
+    of every group. Against the oracle, an empty group leaves C, and each group
+    equals the dense 1D1D call on its slice bit for bit."""
+    ks, m, n = [512, 0, 384, 1024, 128, 256, 640, 768], 1024, 768
+    print(f'k-grouped chunked ks={ks} m={m} n={n}', flush=True)
+    qa, sfa, qb, sfb, c_np = k_grouped_inputs(ks, m, n, 77)
+    ref = ogemm.gemm_k_grouped(qa, sfa, qb, sfb, ks, c_np, oquant.dequant_per_token)
+    d = f32(c_np)
+    layout = torch.tensor(ks, dtype=torch.int32, device=DEV)
+    deep_gemm.k_grouped_fp8_gemm_nt_contiguous((e4m3(qa), f32(sfa)), (e4m3(qb), f32(sfb)), d, ks, layout, d)
+    torch.cuda.synchronize()
+    out = d.cpu().numpy()
+    diff = ogemm.calc_diff(out, ref)
+    print(f'  calc_diff {diff:.3e}', flush=True)
+    assert diff < 1e-3
+    kb0 = 0
+    for g, k in enumerate(ks):
+        if k == 0:
+            assert np.array_equal(out[g], c_np[g])
+            continue
+        off = sum(ks[:g])
+        a_g = qa[off * m:(off + k) * m].reshape(m, k)
+        b_g = qb[off * n:(off + k) * n].reshape(n, k)
+        dd = f32(c_np[g])
+        deep_gemm.fp8_gemm_nt((e4m3(a_g), f32(sfa[:, kb0:kb0 + k // 128])), (e4m3(b_g), f32(sfb[:, kb0:kb0 + k // 128])),
+                              dd, c=dd, recipe=(1, 1, 128))
+        torch.cuda.synchronize()
+        assert torch.equal(dd.view(torch.int32), d[g].view(torch.int32)), f'group {g}'
+        kb0 += k // 128
