@@ -551,7 +551,7 @@ MAKERS = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(Tr
           'kgrouped': make_kgrouped, 'decode': make_decode}
 # Configurations summarized next to the headline in the default run (per-launch
 # kernel time and roofline fraction; the headline `value` stays config 2).
-EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4', 'decode']
+EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4', 'kgrouped', 'decode']
 
 
 def t_min_us(flops, nbytes):
