@@ -30,8 +30,8 @@ constexpr int kDefaultMKAlignment = 128;
 // (measured on MI355X over the DeepSeek-V3 (N, K) shapes: faster than every
 // tiled configuration up to 64 rows, slower from 128).
 constexpr int kDenseStreamRows = 64;
-// Dense calls of at most 64 rows, and of at most 128 rows with K <= 8192, take the
-// tiny-M kernel (K split over a workgroup's waves, rows split over workgroups)
+// Dense calls of at most 64 rows, and of at most 128 (256, see below) rows with
+// K <= 8192, take the tiny-M kernel (K split over a workgroup's waves, rows split over workgroups)
 // unless the streaming kernel
 // already has this many workgroups (N >= 8192 or so), or the call has more than
 // 32 rows and fewer than 32 K blocks. Measured on MI355X at M = 1, 16, 17, 32
@@ -39,8 +39,13 @@ constexpr int kDenseStreamRows = 64;
 // even at 7168 x 2048 with 64 rows. At 80-128 rows (flushed, per launch) it
 // takes 24-31 us against 46-51 us for the best tiled launch at 2112 x 7168,
 // 14-18 against 45-51 at 576 x 7168 and 21 against 30-34 at 4096 x 4096, ties
-// at 7168 x 2048, and loses at K = 16384 (97-120 against 93-102 us).
+// at 7168 x 2048, and loses at K = 16384 (97-120 against 93-102 us). At 129-256
+// rows it wins only where the tiled launch is small and its own launch fits one
+// round: 160-256 x 576 x 7168 18-24 against 48-50 us, 160-192 x 2112 x 7168 31
+// against 48; it loses at 256 x 2112 (two rounds, 55 against 50) and wherever
+// the tiled launch has 64 tiles or more (N >= 4096).
 constexpr int64_t kTinyMWideMaxK = 8192;
+constexpr int64_t kTinyMWideMaxTiles = 64;   // 128 x 128 tiles of the tiled launch
 constexpr int kTinyMStreamGrid = 64;
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -520,14 +525,21 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         // the rows that exist (16 x 16 x 128 MFMAs up to 16 rows).
         const bool stream_ok = fp8_masked_stream_supported(args) &&
                                (kind == kMasked || (kind == kNormal && m_rows <= kMaskedStreamRows));
-        // Dense calls of at most 64 rows (128 with K <= 8192): K split over the
+        // Dense calls of at most 64 rows (128-256 with K <= 8192): K split over the
         // waves of a workgroup, so the launch has N / 16 or N / 32 workgroups per
         // row group instead of the streaming kernel's N / 128.
+        auto tinym_fits = [&] {   // above 128 rows: a small tiled launch, and one round of tiny-M workgroups
+            if (m_rows <= 128) return true;
+            if (ceil_div(m_rows, 128) * ceil_div(n, 128) >= kTinyMWideMaxTiles) return false;
+            const TileConfig c = choose_tinym(m_rows, n, k, args.grid_limit);
+            return ceil_div(n, c.block_n) * ceil_div(m_rows, c.block_m) <= args.grid_limit;
+        };
         const bool tinym_ok = kind == kNormal && fp8_tinym_supported(args) &&
-                              (tv == 8 || tv == 9 || m_rows <= kTinyMRows || k <= kTinyMWideMaxK);
+                              (tv == 8 || tv == 9 || m_rows <= kTinyMRows ||
+                               (k <= kTinyMWideMaxK && tinym_fits()));
         if (tv == 8 || tv == 9) {   // forced: the tiny-M kernel
             if (!tinym_ok)
-                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 128 rows with "
+                DG_UNSUPPORTED("tile override: the tiny-M kernel runs dense calls of at most 256 rows with "
                                "K % 128 == 0, K <= 32768, BF16 D and no C");
             t = {g_tile_m.load(), g_tile_n.load(), tv};   // rows per workgroup, columns per workgroup
         } else if (tv == 0 && tinym_ok &&

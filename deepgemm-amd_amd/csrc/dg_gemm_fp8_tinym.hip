@@ -1,4 +1,4 @@
-// Dense FP32-scale FP8 GEMM for at most 128 rows of A (gfx950): decode-sized
+// Dense FP32-scale FP8 GEMM for at most 256 rows of A (gfx950): decode-sized
 // fp8_gemm_nt calls, D[m, n] = sum_k A[m, k] B[n, k] with the per-128-K FP32
 // promotion of the reference's 1D2D kernel
 // (deep_gemm/include/deep_gemm/impls/sm90_fp8_gemm_1d2d.cuh:281-345).
@@ -32,7 +32,7 @@
 // grouped differently from the single-pass kernels (per wave, then across
 // waves), so the bits differ from theirs; it is its own configuration
 // (variant 8).
-// Requirements (checked by the host): M <= 128, K a multiple of 128 and at most
+// Requirements (checked by the host): M <= 256, K a multiple of 128 and at most
 // 32768, BF16 D without C, 16-byte aligned A and B rows.
 #include <hip/hip_runtime.h>
 
@@ -45,7 +45,7 @@ namespace {
 using namespace dev;
 
 constexpr int kBK = 128;
-constexpr int kMaxRows = 128;   // M; a workgroup takes at most 64 of the rows
+constexpr int kMaxRows = 256;   // M; a workgroup takes at most 64 of the rows
 constexpr int kMaxKBlocks = 64 * 4;   // a wave's B scales fit one register: 64 blocks of 4 waves
 
 template <int RT, int CG>
@@ -218,7 +218,7 @@ template <int NW, int RT, int CG>
 void launch_cfg(const Fp8GemmArgs& a, hipStream_t stream) {
     const int64_t grid = (a.n + 16 * CG - 1) / (16 * CG);
     const int64_t row_groups = (a.m + 16 * RT - 1) / (16 * RT);   // workgroups of 16 RT rows each
-    DG_CHECK(grid < (int64_t)1 << 31 && row_groups <= 8);
+    DG_CHECK(grid < (int64_t)1 << 31 && row_groups <= 16);
     hipLaunchKernelGGL((fp8_gemm_tinym_kernel<NW, RT, CG>), dim3((unsigned)grid, (unsigned)row_groups), dim3(NW * 64),
                        0, stream, a);
 }

@@ -91,8 +91,8 @@ struct TileConfig {
     int variant = 1;
 };
 
-// Dense calls of at most 128 rows with K split over the waves of a workgroup
-// (dg_gemm_fp8_tinym.hip): M <= 128, K % 128 == 0, BF16 D, no C; a workgroup
+// Dense calls of at most 256 rows with K split over the waves of a workgroup
+// (dg_gemm_fp8_tinym.hip): M <= 256, K % 128 == 0, BF16 D, no C; a workgroup
 // takes at most kTinyMRows of the rows.
 constexpr int kTinyMRows = 64;
 bool fp8_tinym_supported(const Fp8GemmArgs& a);

@@ -569,12 +569,13 @@ def test_dense_tiny_m_on_stream_kernel(m):
 @pytest.mark.parametrize('m,n,k', [(1, 2112, 7168), (5, 2112, 7168), (16, 7168, 2048), (3, 104, 384),
                                    (16, 24576, 1536), (7, 4096, 16384), (1, 576, 128), (33, 2112, 7168),
                                    (64, 2112, 7168), (50, 104, 1024), (17, 4096, 4096), (3, 104, 32768),
-                                   (96, 2112, 7168), (128, 576, 4096), (100, 104, 1024)])   # two to eight row groups
+                                   (96, 2112, 7168), (128, 576, 4096), (100, 104, 1024),   # two to eight row groups
+                                   (160, 576, 4096), (256, 104, 1024)])                     # up to sixteen
 def test_dense_tiny_m_split_k_kernel(m, n, k):
     """The tiny-M kernel (K split over the waves of a workgroup, partial sums
     added in wave order; up to four 16-row tiles per workgroup), in each of its
     configurations (8 or 4 waves; 16, 32 or 64 columns and 16, 32 or 64 rows per
-    workgroup, 64 columns up to 32 rows; M up to 128): the oracle within one BF16 ulp plus
+    workgroup, 64 columns up to 32 rows; M up to 256): the oracle within one BF16 ulp plus
     2^-15 x sum |a b|, ragged M and N (104, not a multiple of 16 or 32), fewer K
     blocks than waves (K = 128, 384), the largest K (256 blocks: 64 per wave at 4
     waves), MN-major SFA equal to K-major, bitwise-identical reruns, and the same
