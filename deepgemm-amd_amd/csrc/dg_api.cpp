@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <tuple>
 
 #include "dg_internal.hpp"
 
@@ -33,8 +34,7 @@ constexpr int kDenseStreamRows = 64;
 // Dense calls of at most 64 rows, and of at most 128 (256, see below) rows with
 // K <= 8192, take the tiny-M kernel (K split over a workgroup's waves, rows split over workgroups)
 // unless the streaming kernel
-// already has this many workgroups (N >= 8192 or so), or the call has more than
-// 32 rows and fewer than 32 K blocks. Measured on MI355X at M = 1, 16, 17, 32
+// already has this many workgroups (N >= 8192 or so). Measured on MI355X at M = 1, 16, 17, 32
 // and 64: 1.2-2.6x faster for N <= 7168, slower at N = 24576 and 32768 and
 // even at 7168 x 2048 with 64 rows. At 80-128 rows (flushed, per launch) it
 // takes 24-31 us against 46-51 us for the best tiled launch at 2112 x 7168,
@@ -390,7 +390,8 @@ int64_t dense_split_columns(int64_t m_rows, int64_t n, int64_t k, int cus) {
 // bitwise that of one launch. Returns r1 and the second launch's tile, or 0 when
 // the per-round cost model gains less than 5% or K is under 4096 (as for the
 // column split).
-int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int align_m, TileConfig& hi_tile) {
+int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int align_m, TileConfig& hi_tile,
+                              bool bn256_only = false) {
     if (k < 4096) return 0;
     struct Part { int bm, bn; double eff; };
     static const Part parts[] = {{256, 128, 1.00}, {128, 256, 0.97}, {128, 128, 0.80}};   // as in choose_tile_1d2d
@@ -404,6 +405,7 @@ int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int
     for (int64_t mb1 = mb - 1; mb1 >= 1; --mb1)
         for (const auto& p : parts) {
             if (!grouped_tile_ok(kContiguous, 2, p.bm, align_m)) continue;
+            if (bn256_only && p.bn != 256) continue;
             const int64_t rows2 = m_rows - mb1 * 256;
             const double cost = rounds(mb1 * ceil_div(n, 256)) * t256 +
                                 rounds(ceil_div(rows2, p.bm) * ceil_div(n, p.bn)) * (p.bm * p.bn / p.eff);
@@ -796,6 +798,159 @@ void masked_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_
              expected_m, ep);
 }
 
+// ---------------------------------------------------------------- fused L1 (SwiGLU epilogue)
+
+// The L1 grouped GEMM of an MoE layer with the SwiGLU x routing weight -> FP8
+// step in its epilogue: no BF16 intermediate goes through HBM. The reference
+// fuses the same step into its SM100 Mega-MoE kernel's L1 epilogue
+// (deep_gemm/include/deep_gemm/impls/sm100_fp8_fp4_mega_moe.cuh:1066-1130) and
+// runs it unfused between two grouped GEMMs on SM90 (tests/test_mega_moe.py:296-330).
+// Checks: the m-grouped GEMM's (contiguous_impl / masked_impl) for A, B and the
+// layout; B has N = 2I rows with gate and up interleaved in 128-row blocks;
+// q e4m3 [.., rows, I] with unit stride along I and 8-byte aligned rows; sf f32
+// [.., rows, I/128] in any strides; row weights f32 [.., rows] contiguous or null.
+bool contiguous_view(const View& t);
+
+void swiglu_l1_impl(GemmKind kind, const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_,
+                    const dg_tensor* sfb_, const dg_tensor* layout_, int expected_m, const dg_tensor* w_, float clamp,
+                    const dg_tensor* q_, const dg_tensor* sfq_, int ensure_zero_padding, hipStream_t stream) {
+    const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
+               gl = view(layout_, kind == kMasked ? "masked_m" : "grouped_layout"), q = view(q_, "q"),
+               sfq = view(sfq_, "sf");
+    const bool masked = kind == kMasked;
+    DG_CHECK(is_k_major(a) && is_k_major(b));
+    DG_CHECK(a.dtype() == DG_E4M3 && b.dtype() == DG_E4M3);
+    DG_CHECK(gl.dim() == 1 && (gl.size(0) <= 1 || gl.stride(0) == 1));
+    DG_CHECK(gl.dtype() == DG_I32 && gl.on_device());
+    int64_t g = 1, m, k, n, k_;
+    if (masked) {
+        check_grouped_ab(a, g, m, k);
+        int64_t g_;
+        check_grouped_ab(b, g_, n, k_);
+        DG_CHECK(g == g_ && gl.size(0) == g);
+        DG_CHECK(expected_m > 0);
+    } else {
+        std::tie(m, k) = check_ab(a);
+        check_grouped_ab(b, g, n, k_);
+        DG_CHECK(gl.size(0) == (kind == kPsum ? g : m));
+    }
+    DG_CHECK(k == k_ && n > 0 && k > 0 && g > 0 && m >= 0);
+    if (n % 256 != 0) DG_UNSUPPORTED("fused SwiGLU: N = 2 * intermediate must be a multiple of 256");
+    const int64_t inter = n / 2;
+    // q and sf: [rows, I] / [G, max_m, I]
+    check_shape(q, masked ? 3 : 2);
+    DG_CHECK(q.dtype() == DG_E4M3 && q.stride(-1) == 1 && q.size(-1) == inter && q.size(-2) == m);
+    if (masked) DG_CHECK(q.size(0) == g);
+    const int64_t ldq = q.stride(-2), q_gs = masked ? q.stride(0) : 0;
+    DG_CHECK(reinterpret_cast<uintptr_t>(q.data()) % 8 == 0 && (m <= 1 || ldq % 8 == 0) && q_gs % 8 == 0);
+    check_shape(sfq, masked ? 3 : 2);
+    DG_CHECK(sfq.dtype() == DG_F32 && sfq.size(-1) == inter / 128 && sfq.size(-2) == m);
+    if (masked) DG_CHECK(sfq.size(0) == g);
+    const float* w = nullptr;
+    int64_t w_gs = 0;
+    if (w_) {
+        const View wv = view(w_, "row_weights");
+        DG_CHECK(wv.dtype() == DG_F32 && wv.on_device() && contiguous_view(wv));
+        if (masked) {
+            DG_CHECK((wv.dim() == 2 && wv.size(0) == g && wv.size(1) == m) || (wv.dim() == 1 && wv.size(0) == g * m));
+            w_gs = m;
+        } else {
+            DG_CHECK(wv.dim() == 1 && wv.size(0) == m);
+        }
+        w = static_cast<const float*>(wv.data());
+    }
+    if (m == 0) return;
+    const Recipe r = resolve_recipe(nullptr, sfa, sfb);
+    const Operands o{a, sfa, b, sfb, q, nullptr, layout_};
+    if (!is_1d2d(o, r)) DG_UNSUPPORTED("fused SwiGLU: FP32 scales of the (1, 128, 128) recipe");
+    check_sf_layout(sfa, m, k, 1, 128, masked ? g : -1);
+    check_sf_layout(sfb, n, k, 128, 128, g);
+    if (k % 16 != 0) DG_UNSUPPORTED("K must be a multiple of 16 on the FP32-scale FP8 path");
+    check_vector_alignment(a, "a");
+    check_vector_alignment(b, "b");
+    const int align_m = g_mk_alignment.load();
+    Fp8GemmArgs args{};
+    args.a = static_cast<const uint8_t*>(a.data());
+    args.b = static_cast<const uint8_t*>(b.data());
+    args.sfa = static_cast<const float*>(sfa.data());
+    args.sfb = static_cast<const float*>(sfb.data());
+    args.layout = static_cast<const int32_t*>(gl.data());
+    args.m = (int32_t)m, args.n = (int32_t)n, args.k = (int32_t)k;
+    args.num_groups = (int32_t)g;
+    args.align_m = align_m;
+    args.zero_padding = kind == kPsum && ensure_zero_padding;
+    args.lda = a.stride(-2), args.ldb = b.stride(-2);
+    args.a_gs = masked ? a.stride(0) : 0;
+    args.b_gs = b.stride(0);
+    args.sfa_sm = sfa.stride(-2), args.sfa_sk = sfa.stride(-1);
+    args.sfa_gs = masked ? sfa.stride(0) : 0;
+    args.sfb_sn = sfb.stride(-2), args.sfb_sk = sfb.stride(-1), args.sfb_gs = sfb.stride(0);
+    args.grid_limit = 256;
+    try { args.grid_limit = num_sms_now(); } catch (const Error&) {}
+    args.sw_q = static_cast<uint8_t*>(const_cast<void*>(q.data()));
+    args.sw_ldq = ldq, args.sw_q_gs = q_gs;
+    args.sw_sf = static_cast<float*>(const_cast<void*>(sfq.data()));
+    args.sw_sf_sm = sfq.stride(-2), args.sw_sf_sk = sfq.stride(-1), args.sw_sf_gs = masked ? sfq.stride(0) : 0;
+    args.sw_w = w, args.sw_w_gs = w_gs;
+    args.sw_clamp = clamp > 0.f ? clamp : 0.f;
+
+    // Tile: the 256-column tiles of the pipelined kernel (256 rows when K % 128 == 0
+    // and the layout allows, else 128), or for masked decode groups the
+    // weight-streaming kernel with 8 waves (256 columns).
+    const int tv = g_tile_variant.load(), tm = g_tile_m.load(), tn = g_tile_n.load();
+    const bool ktail = k % 128 != 0;
+    if (ceil_div(k, 128) > 1024) DG_UNSUPPORTED("fused SwiGLU: K up to 131072");
+    TileConfig t{256, 256, 2};
+    if (kind == kPsum && (align_m % 256 != 0 || ktail)) t.block_m = 128;
+    if (kind == kContiguous && ktail) t.block_m = 128;
+    if (masked && ktail) t.block_m = 128;
+    const bool stream_ok = masked && fp8_masked_stream_supported(args);
+    if (tv == 5) {
+        if (!stream_ok || tn != 256)
+            DG_UNSUPPORTED("tile override: the fused SwiGLU epilogue takes the streaming kernel with 8 waves, "
+                           "masked layout, K % 128 == 0");
+        t = {kMaskedStreamRows, 256, 5};
+    } else if (tv == 2) {
+        if (tn != 256 || (tm != 256 && tm != 128) || (tm == 256 && ktail))
+            DG_UNSUPPORTED("tile override: the fused SwiGLU epilogue takes 256 x 256 (K % 128 == 0) or 128 x 256 tiles");
+        t = {tm, 256, 2};
+    } else if (tv != 0) {
+        DG_UNSUPPORTED("tile override: the fused SwiGLU epilogue runs variants 2 and 5");
+    } else if (stream_ok && expected_m <= kMaskedStreamRows) {
+        t = {kMaskedStreamRows, 256, 5};
+    }
+    if (t.variant == 2 && !grouped_tile_ok(kind, 2, t.block_m, align_m))
+        DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 128 for the fused SwiGLU epilogue");
+    record_config("fp8_gemm_1d2d_swiglu", kind, t, m, n, k, g);
+    if (t.variant == 5) {
+        launch_fp8_gemm_masked_stream(args, 8, false, stream);
+        return;
+    }
+    if (kind == kContiguous && tv == 0 && t.block_m == 256) {
+        // the row split of the plain contiguous launch, with a 256-column second tile
+        TileConfig ht{};
+        const int64_t r1 = contiguous_split_rows(m, n, k, args.grid_limit, align_m, ht, true);
+        if (r1 > 0) {
+            t_last_config += " split_m=" + std::to_string(r1) + ":" + std::to_string(ht.block_m) + "x" +
+                             std::to_string(ht.block_n);
+            Fp8GemmArgs lo = args;
+            lo.m = (int32_t)r1;
+            launch_fp8_gemm_1d2d_v2(kind, t, lo, stream);
+            Fp8GemmArgs hi = args;
+            hi.m = (int32_t)(m - r1);
+            hi.a = args.a + r1 * args.lda;
+            hi.sfa = args.sfa + r1 * args.sfa_sm;
+            hi.layout = args.layout + r1;
+            hi.sw_q = args.sw_q + r1 * args.sw_ldq;
+            hi.sw_sf = args.sw_sf + r1 * args.sw_sf_sm;
+            if (args.sw_w) hi.sw_w = args.sw_w + r1;
+            launch_fp8_gemm_1d2d_v2(kind, ht, hi, stream);
+            return;
+        }
+    }
+    launch_fp8_gemm_1d2d_v2(kind, t, args, stream);
+}
+
 // ---------------------------------------------------------------- SF layouts
 
 // csrc/apis/layout.hpp:11-58 (planning half).
@@ -1064,6 +1219,7 @@ void moe_combine_impl(const dg_tensor* y_, const dg_tensor* pos_, const dg_tenso
     p.ldy = y.stride(-2);
     p.y_gs = y.dim() == 3 ? y.stride(0) : 0;
     p.max_m = y.dim() == 3 ? (int32_t)y.size(1) : 0;
+    p.rows = y.dim() == 3 ? y.size(0) * y.size(1) : y.size(0);
     p.pos = static_cast<const int32_t*>(pos.data());
     if (w_) {
         const View w = view(w_, "topk_weights");
@@ -1231,6 +1387,27 @@ int dg_m_grouped_fp8_fp4_gemm_nt_masked(const dg_tensor* a, const dg_tensor* sfa
     return guarded([&] {
         masked_impl(a, sfa, b, sfb, d, masked_m, expected_m, recipe, disable_ue8m0_cast, epilogue,
                     static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_m_grouped_fp8_gemm_nt_contiguous_swiglu(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
+                                               const dg_tensor* sfb, const dg_tensor* grouped_layout,
+                                               const dg_tensor* row_weights, float clamp_value, const dg_tensor* q,
+                                               const dg_tensor* sf, int32_t use_psum_layout,
+                                               int32_t ensure_zero_padding, void* stream) {
+    return guarded([&] {
+        swiglu_l1_impl(use_psum_layout ? kPsum : kContiguous, a, sfa, b, sfb, grouped_layout, -1, row_weights,
+                       clamp_value, q, sf, ensure_zero_padding, static_cast<hipStream_t>(stream));
+    });
+}
+
+int dg_m_grouped_fp8_gemm_nt_masked_swiglu(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
+                                           const dg_tensor* sfb, const dg_tensor* masked_m, int32_t expected_m,
+                                           const dg_tensor* row_weights, float clamp_value, const dg_tensor* q,
+                                           const dg_tensor* sf, void* stream) {
+    return guarded([&] {
+        swiglu_l1_impl(kMasked, a, sfa, b, sfb, masked_m, expected_m, row_weights, clamp_value, q, sf, 0,
+                       static_cast<hipStream_t>(stream));
     });
 }
 

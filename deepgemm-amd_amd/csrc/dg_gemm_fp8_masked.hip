@@ -49,6 +49,7 @@
 #include "dg_kernel_common.hpp"
 #include "dg_epilogue.hpp"
 #include "dg_lds_dma.hpp"
+#include "dg_swiglu.hpp"
 
 namespace dgm {
 namespace {
@@ -125,7 +126,9 @@ struct BList {
 // wait for them, and the NW compute waves issue no vector-memory instruction
 // in the K loop, so a load queue that is full never holds a wave that has
 // MFMAs to issue. Both roles meet at one barrier per K block.
-template <int NW, int NRT, int NL>
+// EPI = 1: the fused SwiGLU -> FP8 epilogue (NW = 8: the workgroup's 256 columns
+// are 128 gate and 128 up columns of interleaved weight blocks, dg_swiglu.hpp).
+template <int NW, int NRT, int NL, int EPI = 0>
 __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem, const uint8_t* b_t,
                                             const uint32_t (&voff_b)[BList<NW, NL>::BL], bool b_primed, int g,
                                             int n0, int r0, int a_rows, int m_g, int wave, int lane) {
@@ -228,6 +231,7 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
         // No stage load may still be writing LDS when the epilogue reuses it.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        if constexpr (EPI) __syncthreads();   // (the compute waves' barrier between the epilogue's phases)
         return;
     }
 
@@ -335,13 +339,31 @@ __device__ __forceinline__ void masked_pass(const Fp8GemmArgs& p, uint8_t* smem,
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 
-    Tile t{};
-    t.g = g, t.expert = g, t.m0 = r0, t.n0 = n0, t.row_end = m_g, t.active = 1;
-    using Epi = RowEpilogue<kMasked, 0, 0, NRT, 1>;
-    constexpr int REGION = kLds / NW / 16 * 16;
-    Epi::template run<Epi::rows_per_pass(REGION)>(fin, smem + wave * REGION, lane, t, p.m, p.layout, r0,
-                                                  n0 + wave * 32, p.n, r0, r0 + ROWS, p.d, nullptr, p.ldd, 0,
-                                                  (int64_t)g * p.d_gs);
+    if constexpr (EPI) {
+        static_assert(NW == 8, "256 columns: 128 gate + 128 up");
+        using Buf = SwigluTile<ROWS>;
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                Buf::put4(smem, rt * 32 + lrow, wave * 32 + q * 8 + lhalf * 4, fin[rt][0][q * 4],
+                          fin[rt][0][q * 4 + 1], fin[rt][0][q * 4 + 2], fin[rt][0][q * 4 + 3]);
+        __syncthreads();
+        const SwigluOut o{p.sw_q, p.sw_ldq, p.sw_q_gs, p.sw_sf, p.sw_sf_sm, p.sw_sf_sk,
+                          p.sw_sf_gs, p.sw_w, p.sw_w_gs, p.sw_clamp};
+        Buf::template run<NW>(smem, wave, lane, r0, g, n0 >> 8, o, [&](int m, bool& st, bool& z) {
+            st = m < m_g;
+            z = false;
+        });
+    } else {
+        Tile t{};
+        t.g = g, t.expert = g, t.m0 = r0, t.n0 = n0, t.row_end = m_g, t.active = 1;
+        using Epi = RowEpilogue<kMasked, 0, 0, NRT, 1>;
+        constexpr int REGION = kLds / NW / 16 * 16;
+        Epi::template run<Epi::rows_per_pass(REGION)>(fin, smem + wave * REGION, lane, t, p.m, p.layout, r0,
+                                                      n0 + wave * 32, p.n, r0, r0 + ROWS, p.d, nullptr, p.ldd, 0,
+                                                      (int64_t)g * p.d_gs);
+    }
 }
 
 // One pass over rows [r0, r0 + 16) of the group (a_rows <= 16 of them valid)
@@ -469,11 +491,12 @@ __device__ __forceinline__ void masked_pass16(const Fp8GemmArgs& p, uint8_t* sme
 // M16: passes of at most 16 rows take the 16 x 16 x 128 pass (a separate
 // instantiation, so the 32-row passes keep their register allocation when it is off).
 // NL: loader waves of the 32-row passes (launched with NW + NL waves; not with M16).
-template <int NW, int M16, int NL>
+template <int NW, int M16, int NL, int EPI = 0>
 __global__ void __launch_bounds__((NW + NL) * 64, 1)
 fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
     static_assert(NW >= 4 && NW <= 8, "4 to 8 waves");
     static_assert(!(M16 && NL), "the 16-row pass has no loader waves");
+    static_assert(!EPI || (NW == 8 && !M16), "SwiGLU epilogue: 256 columns, 32-row passes");
     using S = StreamShape<NW>;
     using BLS = BList<NW, NL>;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
@@ -517,11 +540,11 @@ fp8_gemm_masked_stream_kernel(const Fp8GemmArgs p, const int num_n_tiles) {
             }
         }
         switch (nrt) {
-            case 1: masked_pass<NW, 1, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            case 2: masked_pass<NW, 2, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            case 3: masked_pass<NW, 3, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            case 4: masked_pass<NW, 4, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
-            default: masked_pass<NW, 5, NL>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 1: masked_pass<NW, 1, NL, EPI>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 2: masked_pass<NW, 2, NL, EPI>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 3: masked_pass<NW, 3, NL, EPI>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            case 4: masked_pass<NW, 4, NL, EPI>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
+            default: masked_pass<NW, 5, NL, EPI>(p, smem, b_t, voff_b, primed, g, n0, r0, a_rows, m_g, wave, lane); break;
         }
     }
 }
@@ -533,7 +556,13 @@ void launch_nw(const Fp8GemmArgs& a, int mfma16, hipStream_t stream) {
     const int64_t grid = (int64_t)num_n_tiles * a.num_groups;
     if (grid == 0) return;
     DG_CHECK(grid < (int64_t)1 << 31);
-    if (mfma16)
+    if (a.sw_q) {
+        if constexpr (NW == 8)
+            hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 0, kMaskedLoaders, 1>), dim3((unsigned)grid),
+                               dim3((NW + kMaskedLoaders) * 64), 0, stream, a, num_n_tiles);
+        else
+            DG_UNSUPPORTED("the fused SwiGLU epilogue runs the streaming kernel with 8 waves (256 columns)");
+    } else if (mfma16)
         hipLaunchKernelGGL((fp8_gemm_masked_stream_kernel<NW, 1, 0>), dim3((unsigned)grid), dim3(NW * 64), 0, stream,
                            a, num_n_tiles);
     else

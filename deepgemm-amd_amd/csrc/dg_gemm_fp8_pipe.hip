@@ -44,6 +44,7 @@
 #include "dg_kernel_common.hpp"
 #include "dg_epilogue.hpp"
 #include "dg_lds_dma.hpp"
+#include "dg_swiglu.hpp"
 
 namespace dgm {
 namespace {
@@ -70,8 +71,11 @@ __device__ __forceinline__ int swz_g(int r) { return ((r >> 1) ^ ((r & 1) << 2))
 // block, as many L2 requests as the whole A and B tiles; instead each row's scales
 // for KSA K blocks (a "scale group", 16 or 32 bytes, one L2 request) are fetched
 // into a three-slot LDS ring, and the stages carry no SFA.
+// EPI: 0 = the row epilogue (D, optionally + C); 1 = the fused SwiGLU -> FP8
+// epilogue of an m-grouped L1 GEMM (256-column tiles of interleaved gate/up
+// blocks; dg_swiglu.hpp).
 template <int BM, int BN, int WGM, int WGN, int STAGES, int KIND, int OUT_F32, int HAS_C, int KT, int PERSIST,
-          int SB1D = 0, int KSA = 0>
+          int SB1D = 0, int KSA = 0, int EPI = 0>
 // (Four-wave 1D1D tiles run two workgroups per CU: at most 256 registers.)
 __global__ void __launch_bounds__(WGM * WGN * 64, (WGM * WGN == 4 && SB1D) ? 2 : 1)
 fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const int num_n_blocks,
@@ -105,6 +109,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     constexpr bool SPLIT_SB = !SB1D && !(BN % 128 == 0 && WN <= 128 && 128 % WN == 0);
     static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
     static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
+    static_assert(!EPI || (BN == 256 && !PERSIST && !SB1D && !OUT_F32 && !HAS_C &&
+                           (KIND == kContiguous || KIND == kMasked || KIND == kPsum) &&
+                           STAGES * STAGE_BYTES >= SwigluTile<BM>::kBytes),
+                  "SwiGLU epilogue: m-grouped 256-column tiles whose stage ring holds the BF16 tile");
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE_BYTES];
     // SFB of the block's (at most two) 128-row N groups (KSA kernels: K up to 32768,
@@ -136,8 +144,19 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     } else {
         static_cast<Tile&>(t) = decode_tile<BM, BN, KIND, NT>(p.m, p.n, p.num_groups, p.layout, p.align_m,
                                                               p.zero_padding, num_m_blocks, num_n_blocks,
-                                                              static_cast<uint16_t*>(p.d), p.ldd, &s_flag, raster_gm);
-        if (!t.active) return;
+                                                              EPI ? nullptr : static_cast<uint16_t*>(p.d), p.ldd,
+                                                              &s_flag, raster_gm);
+        if (!t.active) {
+            if constexpr (EPI && KIND == kPsum) {
+                // padding rows of a block past its group's rows (ensure_zero_padding)
+                const int r_hi = min(t.m0 + BM, t.pad_end);
+                if (r_hi > t.m0)
+                    swiglu_zero_rows<NT>(SwigluOut{p.sw_q, p.sw_ldq, p.sw_q_gs, p.sw_sf, p.sw_sf_sm, p.sw_sf_sk,
+                                                   p.sw_sf_gs, p.sw_w, p.sw_w_gs, p.sw_clamp},
+                                         0, t.n0 >> 8, t.m0, r_hi, (int)threadIdx.x);
+            }
+            return;
+        }
     }
     const int m0 = t.m0, n0 = t.n0;
 
@@ -660,7 +679,30 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // Epilogue through LDS (row-coalesced stores): every wave is done with the
     // stage ring after this barrier; each then owns NW-th of the LDS.
     __syncthreads();
-    {
+    if constexpr (EPI) {
+        // Phase 1: the tile's outputs as BF16 into LDS (the stage ring is free);
+        // phase 2: per row, y = silu(gate) * up * w over the tile's 128
+        // intermediate columns, quantized per token into q and sf.
+        using Buf = SwigluTile<BM>;
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+            for (int j = 0; j < SN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    Buf::put4(smem, wm * WM + i * 32 + lrow, wn * WN + j * 32 + q * 8 + lhalf * 4, fin[i][j][q * 4],
+                              fin[i][j][q * 4 + 1], fin[i][j][q * 4 + 2], fin[i][j][q * 4 + 3]);
+        __syncthreads();
+        const int m_lo = npass == 2 ? m0 + pass * 128 : m0;
+        const int m_hi = npass == 2 ? m_lo + 128 : m0 + BM;
+        const SwigluOut o{p.sw_q, p.sw_ldq, p.sw_q_gs, p.sw_sf, p.sw_sf_sm, p.sw_sf_sk,
+                          p.sw_sf_gs, p.sw_w, p.sw_w_gs, p.sw_clamp};
+        Buf::template run<NW>(smem, wave, lane, m0, KIND == kMasked ? t.g : 0, n0 >> 8, o,
+                              [&](int m, bool& st, bool& z) {
+                                  row_predicate<KIND>(t, p.m, p.layout, m, st, z);
+                                  if (m < m_lo || m >= m_hi) st = z = false;
+                              });
+    } else {
         using Epi = RowEpilogue<KIND, OUT_F32, HAS_C, SM, SN>;
         constexpr int REGION = (STAGES * STAGE_BYTES / NW) / 16 * 16;
         const int64_t d_goff = (KIND == kMasked || KIND == kKGrouped) ? (int64_t)t.g * p.d_gs : 0;
@@ -729,7 +771,22 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
             hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST>), gdim, \
                                bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
     } while (0)
-    if constexpr (KIND != kNormal) {
+    if (a.sw_q) {   // fused SwiGLU -> FP8 epilogue (m-grouped 256-column tiles)
+        if constexpr (BN == 256 && !PERSIST && (KIND == kContiguous || KIND == kMasked || KIND == kPsum)) {
+            if (k_tail)
+                hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 1, 0, 0, 0, 1>),
+                                   gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+            else if (ksa == 4)
+                hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 0, 0, 0,
+                                                              KSA_OK ? 4 : 0, 1>),
+                                   gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+            else
+                hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 0, 0, 0, 0, 1>),
+                                   gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+        } else {
+            DG_UNSUPPORTED("the fused SwiGLU epilogue runs m-grouped 256-column tiles");
+        }
+    } else if constexpr (KIND != kNormal) {
         DG_CHECK(!a.out_f32 && a.c == nullptr);
         DG_PIPE_LAUNCH(0, 0);
     } else if (a.out_f32) {

@@ -77,6 +77,17 @@ struct Fp8GemmArgs {
     int64_t sfa_sm, sfa_sk, sfa_gs;
     int64_t sfb_sn, sfb_sk, sfb_gs;
     int32_t grid_limit;        // persistent kernels: workgroups to launch at most (the CU count)
+    // Fused SwiGLU epilogue of an m-grouped L1 GEMM (sw_q != null; d unused):
+    // N = 2I with gate and up interleaved in 128-row blocks, and instead of D the
+    // kernel writes q = e4m3(silu(gate) * up * w / sf) [.., rows, I] and the 1 x 128
+    // scales sf [.., rows, I/128] (dg_swiglu.hpp).
+    uint8_t* sw_q;
+    int64_t sw_ldq, sw_q_gs;           // bytes
+    float* sw_sf;
+    int64_t sw_sf_sm, sw_sf_sk, sw_sf_gs;
+    const float* sw_w;                 // row weights [.., rows] or null (1)
+    int64_t sw_w_gs;
+    float sw_clamp;                    // <= 0: no clamp
 };
 
 struct TileConfig {
@@ -245,6 +256,7 @@ struct CombineArgs {
     const uint16_t* y;         // bf16 rows [rows, n] or [E, max_m, n]
     int64_t ldy, y_gs;         // elements
     int32_t max_m;             // 0: flat rows; else rows r = e * max_m + i
+    int64_t rows;              // rows of y (E * max_m for [E, max_m, n]): pos entries past it are skipped
     const int32_t* pos;        // [t, k] contiguous
     const float* topk_w;       // [t, k] or null
     int64_t w_st, w_sk;

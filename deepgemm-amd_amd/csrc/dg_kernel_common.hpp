@@ -167,7 +167,7 @@ __device__ __forceinline__ Tile decode_tile(int m, int n, int num_groups, const 
         t.pad_end = zero_padding ? aend : 0;
         if (t.m0 >= end) {
             t.active = 0;
-            if (zero_padding) {
+            if (zero_padding && zero_d) {   // (null: the caller writes its own zero rows)
                 const int r_hi = min(t.m0 + BM, aend);
                 for (int idx = threadIdx.x; idx < (r_hi - t.m0) * BN; idx += NT) {
                     const int r = t.m0 + idx / BN, c = t.n0 + idx % BN;
@@ -256,7 +256,7 @@ __device__ __forceinline__ PTile decode_tile_persistent(int lt, int m, int n, in
         t.pad_end = zero_padding ? aend : 0;
         if (t.m0 >= end) {
             t.active = 0;
-            if (zero_padding) {
+            if (zero_padding && zero_d) {   // (null: the caller writes its own zero rows)
                 const int r_hi = min(t.m0 + BM, aend);
                 for (int idx = threadIdx.x; idx < (r_hi - t.m0) * BN; idx += NT) {
                     const int r = t.m0 + idx / BN, c = t.n0 + idx % BN;

@@ -24,6 +24,7 @@
 #include <mutex>
 
 #include "dg_internal.hpp"
+#include "dg_swiglu.hpp"
 
 namespace dgm {
 namespace {
@@ -32,9 +33,15 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ int align_up(int x, int a) { return (x + a - 1) / a * a; }
 
+// Expert id of (token t, slot j); int64 ids outside [0, E) come back as -1
+// (unrouted) before the value is narrowed, so 2^32 + e is not taken for e.
 __device__ __forceinline__ int topk_at(const MoeDispatchArgs& p, int t, int j) {
     const int64_t off = (int64_t)t * p.topk_st + (int64_t)j * p.topk_sk;
-    return p.topk_i64 ? (int)static_cast<const int64_t*>(p.topk)[off] : static_cast<const int32_t*>(p.topk)[off];
+    if (p.topk_i64) {
+        const int64_t e = static_cast<const int64_t*>(p.topk)[off];
+        return (e >= 0 && e < p.num_experts) ? (int)e : -1;
+    }
+    return static_cast<const int32_t*>(p.topk)[off];
 }
 
 __device__ __forceinline__ bool routed(const MoeDispatchArgs& p, int e) { return e >= 0 && e < p.num_experts; }
@@ -182,24 +189,12 @@ __global__ void __launch_bounds__(kThreads) moe_scatter_kernel(const MoeDispatch
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-__device__ __forceinline__ uint32_t e4m3_code_slow(float v) {
-    const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-    const float a = fabsf(v);
-    if (!(a <= 464.0f)) return sign | 0x7Fu;
-    int e = (int)((__float_as_uint(a) >> 23) & 0xFF) - 127;
-    e = e < -6 ? -6 : e;
-    const float r = rintf(a * __uint_as_float((uint32_t)(3 - e + 127) << 23)) * __uint_as_float((uint32_t)(e - 3 + 127) << 23);
-    if (r >= 0.015625f) {
-        const uint32_t rb = __float_as_uint(r);
-        return sign | ((((rb >> 23) & 0xFF) - 127 + 7) << 3) | ((rb >> 20) & 0x7);
-    }
-    return sign | (uint32_t)rintf(r * 512.0f);
-}
-
 // One wave per (row, 512 output columns): lane l owns columns 8l .. 8l + 7 of
 // the slice. gate = x[row, c], up = x[row, I + c]; y = silu(gate) * up * w in
 // float32; then the per-token quantizer (amax over GRAN columns, clamped at
-// 1e-4, sf = amax * fl32(1/448), code = e4m3(y * (1 / sf))).
+// 1e-4, sf = amax * fl32(1/448), code = e4m3(y * (1 / sf))). The arithmetic is
+// dev::swiglu_weighted and dev::quantize_group8, which the GEMMs' fused SwiGLU
+// epilogue calls too.
 template <int GRAN>
 __global__ void __launch_bounds__(kThreads) moe_swiglu_cast_kernel(const SwigluCastArgs p, int slices) {
     constexpr int TPG = GRAN / 8;
@@ -220,46 +215,18 @@ __global__ void __launch_bounds__(kThreads) moe_swiglu_cast_kernel(const SwigluC
         const float w = p.row_weight ? p.row_weight[row] : 1.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            float g = bf16_to_f32(e & 1 ? gw[e >> 1] >> 16 : gw[e >> 1] & 0xFFFFu);
-            float u = bf16_to_f32(e & 1 ? uw[e >> 1] >> 16 : uw[e >> 1] & 0xFFFFu);
-            if (p.clamp > 0.f) {
-                u = fminf(p.clamp, fmaxf(-p.clamp, u));
-                g = fminf(p.clamp, g);
-            }
-            const float s = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
-            y[e] = __fmul_rn(__fmul_rn(s, u), w);
+            const float g = bf16_to_f32(e & 1 ? gw[e >> 1] >> 16 : gw[e >> 1] & 0xFFFFu);
+            const float u = bf16_to_f32(e & 1 ? uw[e >> 1] >> 16 : uw[e >> 1] & 0xFFFFu);
+            y[e] = dev::swiglu_weighted(g, u, w, p.clamp);
         }
     } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = 0.f;
     }
-    float amax = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
-#pragma unroll
-    for (int o = TPG / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-    amax = fmaxf(amax, 1e-4f);
-    const float sf = __fmul_rn(amax, 1.0f / 448.0f);
-    const float inv = __fdiv_rn(1.0f, sf);
-    uint32_t lo = 0, hi = 0;
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(y[e], inv);
-    if (__builtin_expect(__ballot(!(amax < __uint_as_float(0x7F800000u))) == 0, 1)) {
-        int l = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-        l = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], l, true);
-        int h = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], 0, false);
-        h = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], h, true);
-        lo = (uint32_t)l, hi = (uint32_t)h;
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            lo |= e4m3_code_slow(v[e]) << (8 * e);
-            hi |= e4m3_code_slow(v[4 + e]) << (8 * e);
-        }
-    }
+    float sf;
+    const uint2 codes = dev::quantize_group8<TPG>(y, sf);
     if (in) {
-        *reinterpret_cast<uint2*>(p.q + (int64_t)row * p.ldq + col) = uint2{lo, hi};
+        *reinterpret_cast<uint2*>(p.q + (int64_t)row * p.ldq + col) = codes;
         if (lane % TPG == 0)
             p.sf[(int64_t)row * p.sf_sm + (int64_t)(col / GRAN) * p.sf_sk] = sf;
     }
@@ -282,7 +249,7 @@ __global__ void __launch_bounds__(kThreads) moe_combine_kernel(const CombineArgs
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
     for (int j = 0; j < p.k; ++j) {
         const int r = p.pos[(int64_t)t * p.k + j];
-        if (r < 0) continue;
+        if (r < 0 || r >= p.rows) continue;   // unrouted, or not a row of y
         const int64_t off = p.max_m ? (int64_t)(r / p.max_m) * p.y_gs + (int64_t)(r % p.max_m) * p.ldy
                                     : (int64_t)r * p.ldy;
         const uint4 v4 = *reinterpret_cast<const uint4*>(p.y + off + col);

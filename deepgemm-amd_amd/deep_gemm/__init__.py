@@ -535,6 +535,64 @@ def moe_combine(y: torch.Tensor, pos: torch.Tensor, topk_weights: Optional[torch
     return out
 
 
+def transform_l1_weights_for_swiglu(b: Tuple[torch.Tensor, torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(e4m3 [(G,) 2I, K], f32 SF [(G,) 2I/128, K/128]) with the usual [gate | up]
+    rows -> the same weights with gate and up interleaved in blocks of 128 rows
+    (rows [256j, +128) = gate rows [128j, +128), rows [256j + 128, +128) = up rows
+    [128j, +128)), the L1 weight layout of the fused SwiGLU grouped GEMMs. The
+    reference's transform_weights_for_mega_moe interleaves at 8 rows
+    (deep_gemm/mega/__init__.py:112-127) for its per-row FP4 scales; 128 x 128 FP32
+    block scales keep whole 128-row blocks together. Run once per weight load."""
+    w, sf = _pair(b, 'b')
+    squeeze = w.dim() == 2
+    if squeeze:
+        w, sf = w.unsqueeze(0), sf.unsqueeze(0)
+    g, n, k = w.shape
+    if n % 256 != 0 or sf.shape[-2] * 128 != n:
+        raise ValueError('the fused SwiGLU layout needs 2I % 256 == 0 and one SF row per 128 weight rows')
+    nb = n // 256   # 128-row blocks per half
+    wu = w.view(torch.uint8)
+    wi = torch.stack([wu[:, :n // 2].reshape(g, nb, 128, k), wu[:, n // 2:].reshape(g, nb, 128, k)], dim=2)
+    si = torch.stack([sf[:, :nb], sf[:, nb:]], dim=2)
+    wi = wi.reshape(g, n, k).contiguous().view(w.dtype)
+    si = si.reshape(g, 2 * nb, sf.shape[-1]).contiguous()
+    return (wi[0], si[0]) if squeeze else (wi, si)
+
+
+def m_grouped_fp8_gemm_nt_contiguous_swiglu(a, b, out: Tuple[torch.Tensor, torch.Tensor],
+                                            grouped_layout: torch.Tensor, row_weights: Optional[torch.Tensor] = None,
+                                            activation_clamp: Optional[float] = None, use_psum_layout: bool = False,
+                                            ensure_zero_padding: bool = True) -> None:
+    """The L1 grouped GEMM of an MoE layer with SwiGLU x routing weight -> FP8 in its
+    epilogue: out = (e4m3 q [M, I], f32 sf [M, I/128]) receives
+    moe_swiglu_apply_weight_to_fp8(D) of the contiguous grouped GEMM's BF16 D, bit for
+    bit, without D going through HBM (the fusion of the reference's Mega-MoE L1
+    epilogue, sm100_fp8_fp4_mega_moe.cuh:1066-1130). b: transform_l1_weights_for_swiglu
+    output. Rows with grouped_layout == -1 are left untouched."""
+    a_t, sfa = _pair(a, 'a')
+    b_t, sfb = _pair(b, 'b')
+    q, sf = _pair(out, 'out')
+    _check(_lib.dg_m_grouped_fp8_gemm_nt_contiguous_swiglu(
+        _ref(_desc(a_t)), _ref(_desc(sfa)), _ref(_desc(b_t)), _ref(_desc(sfb)), _ref(_desc(grouped_layout)),
+        _opt(row_weights), float(activation_clamp or 0.0), _ref(_desc(q)), _ref(_desc(sf)),
+        int(bool(use_psum_layout)), int(bool(ensure_zero_padding)), _ffi.stream_of(q)))
+
+
+def m_grouped_fp8_gemm_nt_masked_swiglu(a, b, out: Tuple[torch.Tensor, torch.Tensor], masked_m: torch.Tensor,
+                                        expected_m: int, row_weights: Optional[torch.Tensor] = None,
+                                        activation_clamp: Optional[float] = None) -> None:
+    """The masked (decode) form of m_grouped_fp8_gemm_nt_contiguous_swiglu: out =
+    (q [G, max_m, I], sf [G, max_m, I/128]); row_weights [G, max_m] or None. Rows
+    >= masked_m[g] are left untouched."""
+    a_t, sfa = _pair(a, 'a')
+    b_t, sfb = _pair(b, 'b')
+    q, sf = _pair(out, 'out')
+    _check(_lib.dg_m_grouped_fp8_gemm_nt_masked_swiglu(
+        _ref(_desc(a_t)), _ref(_desc(sfa)), _ref(_desc(b_t)), _ref(_desc(sfb)), _ref(_desc(masked_m)),
+        int(expected_m), _opt(row_weights), float(activation_clamp or 0.0), _ref(_desc(q)), _ref(_desc(sf)),
+        _ffi.stream_of(q)))
+
+
 def per_token_cast_to_fp8_mn_major(x: torch.Tensor, use_ue8m0: bool,
                                    gran_k: int = 128) -> Tuple[torch.Tensor, torch.Tensor]:
     """per_token_cast_to_fp8 with the scales written straight into the MN-major

@@ -88,6 +88,8 @@ SIGNATURES = {
     'dg_moe_dispatch_noalloc': (_I, [_T, _T, _T, _T, _I, _I, _I, _T, _T, _T, _T, _T, _V]),
     'dg_moe_swiglu_apply_weight_to_fp8': (_I, [_T, _T, _T, ctypes.c_float, _T, _T, _I, _V]),
     'dg_moe_combine': (_I, [_T, _T, _T, _T, _V]),
+    'dg_m_grouped_fp8_gemm_nt_contiguous_swiglu': (_I, [_T, _T, _T, _T, _T, _T, ctypes.c_float, _T, _T, _I, _I, _V]),
+    'dg_m_grouped_fp8_gemm_nt_masked_swiglu': (_I, [_T, _T, _T, _T, _T, _I, _T, ctypes.c_float, _T, _T, _V]),
     'dg_k_grouped_fp8_gemm_nt_contiguous': (_I, [_T, _T, _T, _T, _T, _P(_I), _I, _T, _T, _P(_I), _I, _V]),
     'dg_k_grouped_fp8_gemm_tn_contiguous': (_I, [_T, _T, _T, _T, _T, _P(_I), _I, _T, _T, _P(_I), _I, _V]),
     'dg_set_num_sms': (_I, [_I]),

@@ -328,6 +328,41 @@ int dg_moe_swiglu_apply_weight_to_fp8(const dg_tensor* x, const dg_tensor* row_w
                                       const dg_tensor* row_layout, float clamp_value, const dg_tensor* q,
                                       const dg_tensor* sf, int32_t gran_k, void* stream);
 
+/* Fused L1 grouped GEMM of an MoE layer: the m-grouped GEMM with the SwiGLU x
+ * routing weight -> FP8 step of dg_moe_swiglu_apply_weight_to_fp8 in its
+ * epilogue, so the BF16 gate/up output never goes through HBM. The reference
+ * fuses the same step into the L1 epilogue of its SM100 Mega-MoE kernel
+ * (deep_gemm/include/deep_gemm/impls/sm100_fp8_fp4_mega_moe.cuh:1066-1130, weights
+ * prepared by transform_weights_for_mega_moe, deep_gemm/mega/__init__.py:112-165).
+ * Results equal dg_moe_swiglu_apply_weight_to_fp8 applied to the BF16 D of the
+ * plain grouped GEMM with the standard [gate | up] weight, bit for bit.
+ *   a, sfa, grouped_layout / masked_m, expected_m, use_psum_layout,
+ *       ensure_zero_padding  as dg_m_grouped_fp8_fp4_gemm_nt_contiguous / _masked
+ *       (FP32 scales, recipe (1, 128, 128))
+ *   b    e4m3 [G, 2I, K], I % 128 == 0, gate and up rows interleaved in blocks of
+ *        128: rows [256j, 256j + 128) = gate rows [128j, +128), rows
+ *        [256j + 128, 256j + 256) = up rows [128j, +128); sfb [G, 2I/128, K/128]
+ *        in the same block order
+ *   row_weights  f32 [M] (masked: [G, max_m]) contiguous, or null (w = 1)
+ *   clamp_value  > 0: up clamped to [-c, c] and gate to <= c; <= 0: no clamp
+ *   q    e4m3 [M, I] (masked: [G, max_m, I]), unit stride along I, 8-byte rows
+ *   sf   f32 [M, I/128] (masked: [G, max_m, I/128]), any strides
+ * Rows the GEMM leaves untouched (m_indices < 0, rows >= masked_m) are not
+ * written; psum padding rows with ensure_zero_padding get zero codes and the
+ * scale of an all-zero row. */
+int dg_m_grouped_fp8_gemm_nt_contiguous_swiglu(const dg_tensor* a, const dg_tensor* sfa,
+                                               const dg_tensor* b, const dg_tensor* sfb,
+                                               const dg_tensor* grouped_layout,
+                                               const dg_tensor* row_weights, float clamp_value,
+                                               const dg_tensor* q, const dg_tensor* sf,
+                                               int32_t use_psum_layout, int32_t ensure_zero_padding,
+                                               void* stream);
+int dg_m_grouped_fp8_gemm_nt_masked_swiglu(const dg_tensor* a, const dg_tensor* sfa,
+                                           const dg_tensor* b, const dg_tensor* sfb,
+                                           const dg_tensor* masked_m, int32_t expected_m,
+                                           const dg_tensor* row_weights, float clamp_value,
+                                           const dg_tensor* q, const dg_tensor* sf, void* stream);
+
 /* Combine: out[t] = sum over slots j in order of w[t, j] * y[pos[t, j]] (w = 1 when
  * topk_weights is null: the weights were applied before the L2 GEMM, as in the
  * reference's pipeline), each step rounded to f32, the result once to bf16.

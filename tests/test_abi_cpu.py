@@ -249,6 +249,76 @@ def test_grouped_validation():
     assert st == _ffi.DG_ERR_INVALID and 'expected_m > 0' in _ffi.lib.dg_last_error().decode()
 
 
+def test_fused_swiglu_host_checks():
+    """dg_m_grouped_fp8_gemm_nt_{contiguous,masked}_swiglu: shape, dtype and layout
+    checks run on the host before any launch."""
+    g, m, inter, k = 4, 512, 256, 1024
+    n = 2 * inter
+    a = fake((m, k), _ffi.DG_E4M3)
+    sfa = fake((m, k // 128), _ffi.DG_F32)
+    b = fake((g, n, k), _ffi.DG_E4M3)
+    sfb = fake((g, n // 128, k // 128), _ffi.DG_F32)
+    idx = fake((m,), _ffi.DG_I32)
+    q = fake((m, inter), _ffi.DG_E4M3)
+    sf = fake((m, inter // 128), _ffi.DG_F32)
+    w = fake((m,), _ffi.DG_F32)
+
+    def contiguous(a=a, b=b, sfb=sfb, q=q, sf=sf, w=w, psum=0):
+        st = _ffi.lib.dg_m_grouped_fp8_gemm_nt_contiguous_swiglu(
+            *(ctypes.byref(x) for x in (a, sfa, b, sfb, idx)), ctypes.byref(w) if w else None, 0.0,
+            ctypes.byref(q), ctypes.byref(sf), psum, 1, None)
+        return st, _ffi.lib.dg_last_error().decode()
+
+    st, msg = contiguous(b=fake((g, 384, k), _ffi.DG_E4M3), sfb=fake((g, 3, k // 128), _ffi.DG_F32))
+    assert st == _ffi.DG_ERR_UNSUPPORTED and 'multiple of 256' in msg
+    st, msg = contiguous(q=fake((m, inter), _ffi.DG_BF16))
+    assert st == _ffi.DG_ERR_INVALID and 'q.dtype() == DG_E4M3' in msg
+    st, msg = contiguous(q=fake((m, n), _ffi.DG_E4M3))
+    assert st == _ffi.DG_ERR_INVALID and 'q.size(-1) == inter' in msg
+    st, msg = contiguous(q=fake((m, inter), _ffi.DG_E4M3, strides=(inter + 4, 1)))
+    assert st == _ffi.DG_ERR_INVALID and 'ldq % 8 == 0' in msg
+    st, msg = contiguous(sf=fake((m, inter // 64), _ffi.DG_F32))
+    assert st == _ffi.DG_ERR_INVALID and 'sfq.size(-1) == inter / 128' in msg
+    st, msg = contiguous(w=fake((m - 1,), _ffi.DG_F32))
+    assert st == _ffi.DG_ERR_INVALID and 'wv.size(0) == m' in msg
+    st, msg = contiguous(psum=1)   # psum: grouped_layout holds one end per group
+    assert st == _ffi.DG_ERR_INVALID and 'gl.size(0) ==' in msg
+    st, msg = contiguous(a=fake((m, k), _ffi.DG_E4M3, device=-1))
+    assert st == _ffi.DG_ERR_INVALID and 'on_device' in msg
+    # 256 x 256 tiles need K % 128 == 0 (the K-tail 256-row schedule is not built)
+    a_t, sfa_t = fake((m, 1040), _ffi.DG_E4M3), fake((m, 9), _ffi.DG_F32)
+    b_t, sfb_t = fake((g, n, 1040), _ffi.DG_E4M3), fake((g, n // 128, 9), _ffi.DG_F32)
+    deep_gemm.set_tile_override(256, 256, variant=2)
+    try:
+        st = _ffi.lib.dg_m_grouped_fp8_gemm_nt_contiguous_swiglu(
+            *(ctypes.byref(x) for x in (a_t, sfa_t, b_t, sfb_t, idx)), None, 0.0, ctypes.byref(q), ctypes.byref(sf),
+            0, 1, None)
+        msg = _ffi.lib.dg_last_error().decode()
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    assert st == _ffi.DG_ERR_UNSUPPORTED and '128 x 256' in msg
+    # masked: q is [G, max_m, I], masked_m has G entries, expected_m > 0
+    max_m = 128
+    a3 = fake((g, max_m, k), _ffi.DG_E4M3)
+    sfa3 = fake((g, max_m, k // 128), _ffi.DG_F32)
+    mm = fake((g,), _ffi.DG_I32)
+    q3 = fake((g, max_m, inter), _ffi.DG_E4M3)
+    sf3 = fake((g, max_m, inter // 128), _ffi.DG_F32)
+
+    def masked(q=q3, expected_m=64, mm=mm):
+        st = _ffi.lib.dg_m_grouped_fp8_gemm_nt_masked_swiglu(
+            *(ctypes.byref(x) for x in (a3, sfa3, b, sfb, mm)), expected_m, None, 0.0, ctypes.byref(q),
+            ctypes.byref(sf3), None)
+        return st, _ffi.lib.dg_last_error().decode()
+
+    st, msg = masked(q=fake((g * max_m, inter), _ffi.DG_E4M3))
+    assert st == _ffi.DG_ERR_INVALID and 'dim() == n' in msg
+    st, msg = masked(expected_m=0)
+    assert st == _ffi.DG_ERR_INVALID and 'expected_m > 0' in msg
+    st, msg = masked(mm=fake((g + 1,), _ffi.DG_I32))
+    assert st == _ffi.DG_ERR_INVALID and 'gl.size(0) == g' in msg
+
+
 def test_plan_sf_transform_kinds():
     def plan(sf, mn, k, recipe3=None, recipe2=None, groups=-1, is_sfa=-1, disable=0):
         kind = ctypes.c_int32(-1)

@@ -59,3 +59,24 @@ def test_calc_diff_and_count_bytes():
     y = torch.randn(1000, dtype=torch.float64)
     assert abs(calc_diff(x, y) - ogemm.calc_diff(x.numpy(), y.numpy())) < 1e-12
     assert count_bytes(torch.empty(10, dtype=torch.bfloat16), (torch.empty(3), None)) == 32
+
+
+def test_transform_l1_weights_for_swiglu_cpu():
+    """The fused SwiGLU weight layout on CPU tensors: rows [256j, +128) are gate rows
+    [128j, +128), rows [256j + 128, +128) up rows [128j, +128) (up = rows [I, 2I)),
+    and each SF row follows its 128-row block; 2-D weights keep their rank."""
+    rng = np.random.default_rng(3)
+    for g in (None, 2):
+        inter, k = 384, 256
+        shape = (2 * inter, k) if g is None else (g, 2 * inter, k)
+        w = torch.from_numpy(rng.integers(0, 126, shape).astype(np.uint8)).view(torch.float8_e4m3fn)
+        sf = torch.from_numpy(rng.random(shape[:-2] + (2 * inter // 128, k // 128)).astype(np.float32))
+        wi, si = deep_gemm.transform_l1_weights_for_swiglu((w, sf))
+        assert wi.shape == w.shape and si.shape == sf.shape and wi.dtype == w.dtype
+        src, dst = w.view(torch.uint8).numpy(), wi.view(torch.uint8).numpy()
+        for j in range(inter // 128):
+            assert np.array_equal(dst[..., 256 * j:256 * j + 128, :], src[..., 128 * j:128 * j + 128, :])
+            assert np.array_equal(dst[..., 256 * j + 128:256 * j + 256, :],
+                                  src[..., inter + 128 * j:inter + 128 * j + 128, :])
+            assert np.array_equal(si.numpy()[..., 2 * j, :], sf.numpy()[..., j, :])
+            assert np.array_equal(si.numpy()[..., 2 * j + 1, :], sf.numpy()[..., inter // 128 + j, :])
