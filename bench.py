@@ -43,7 +43,7 @@ PROFILE_NAMES = {'dense': 'fp8_gemm_nt_dense_m4096', 'dense_acc': 'fp8_gemm_nt_d
                  'contiguous': 'm_grouped_fp8_gemm_nt_contiguous_e8_t32768',
                  'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096',
                  'cast': 'per_token_cast_to_fp8_bf16', 'kgrouped': 'k_grouped_fp8_gemm_nt_e8_m4096_n7168',
-                 'decode': 'fp8_gemm_nt_m64_n2112_k7168'}
+                 'decode': 'fp8_gemm_nt_m64_n2112_k7168', 'moe_l1': 'moe_l1_swiglu_e8_t32768_e16_m256'}
 
 
 def parse():
@@ -52,7 +52,8 @@ def parse():
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--workload', default='dense',
-                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped', 'decode'])
+                    choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped', 'decode',
+                             'moe_l1'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-extras', action='store_true',
                     help='default workload only: skip the per-launch summaries of the other configurations')
@@ -436,6 +437,88 @@ def make_kgrouped():
     return [Launch(f'g{g}_m{m}_n{n}_sumk{sum_k}', mk, 2 * m * n * sum_k, nbytes)], cfg
 
 
+def make_moe_l1():
+    """The L1 (gate/up) grouped GEMM of the MoE layer with its SwiGLU x routing
+    weight -> FP8 step, unfused (BF16 D through HBM, then the cast kernel) and
+    fused (the step in the GEMM's epilogue), at the config 3 (contiguous, N = 4096
+    = 2 x 2048, K = 7168) and config 4 (masked, same N and K) gate/up shapes. All
+    four launches produce the same q and sf bits; FLOPs are the valid rows' GEMM
+    FLOPs, bytes the fused job's (A, B, scales, q and sf)."""
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    c = contiguous_operands(dev)
+    m = masked_operands(dev)
+    co, mo = c['shapes'][0], m['shapes'][0]
+    assert (co['n'], co['k']) == (4096, 7168) and (mo['n'], mo['k']) == (4096, 7168)
+    n, k = co['n'], co['k']
+    inter = n // 2
+    m_pad, idx, total = c['m_pad'], c['m_indices'], c['total']
+    g, max_m, mm, sum_m = m['num_groups'], m['max_m'], m['masked_m_dev'], int(m['masked_m'].sum())
+    gen = torch.Generator().manual_seed(1)
+    rw_c = torch.rand((m_pad,), generator=gen).to(dev)
+    rw_m = torch.rand((g, max_m), generator=gen).to(dev)
+    bf_c = deep_gemm.transform_l1_weights_for_swiglu(co['b'])
+    bf_m = deep_gemm.transform_l1_weights_for_swiglu(mo['b'])
+    sfk = (k + 127) // 128
+
+    def out(rows_shape):
+        return (torch.empty(rows_shape + (inter,), dtype=torch.float8_e4m3fn, device=dev),
+                torch.empty(rows_shape + (inter // 128,), dtype=torch.float32, device=dev))
+
+    def mk_c_unfused():
+        a2, b2 = _twin(co['a']), _twin(co['b'])
+        h = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
+        q, sf = out((m_pad,))
+
+        def run():
+            deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a2, b2, h, idx)
+            names[0] = deep_gemm.get_last_config()
+            deep_gemm.moe_swiglu_apply_weight_to_fp8(h, rw_c, idx, out=(q, sf))
+            names[1] = deep_gemm.get_last_config()
+        names = ['', '']
+        run.config = lambda: ' + '.join(names)
+        return run
+
+    def mk_c_fused():
+        a2, b2 = _twin(co['a']), _twin(bf_c)
+        o = out((m_pad,))
+        return lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous_swiglu(a2, b2, o, idx, rw_c)
+
+    def mk_m_unfused():
+        a2, b2 = _twin(mo['a']), _twin(mo['b'])
+        h = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
+        q, sf = out((g * max_m,))
+
+        def run():
+            deep_gemm.m_grouped_fp8_gemm_nt_masked(a2, b2, h, mm, m['expected_m'])
+            names[0] = deep_gemm.get_last_config()
+            deep_gemm.moe_swiglu_apply_weight_to_fp8(h.view(g * max_m, n), rw_m.view(-1), out=(q, sf))
+            names[1] = deep_gemm.get_last_config()
+        names = ['', '']
+        run.config = lambda: ' + '.join(names)
+        return run
+
+    def mk_m_fused():
+        a2, b2 = _twin(mo['a']), _twin(bf_m)
+        o = out((g, max_m))
+        return lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked_swiglu(a2, b2, o, mm, m['expected_m'], rw_m)
+
+    sf_b = 4 * ((n + 127) // 128) * sfk
+    c_bytes = m_pad * k + 8 * n * k + 4 * m_pad * sfk + 8 * sf_b + 4 * m_pad + m_pad * inter + \
+        4 * m_pad * (inter // 128) + 4 * m_pad
+    m_bytes = g * n * k + sum_m * k + 4 * sum_m * sfk + g * sf_b + sum_m * inter + 4 * sum_m * (inter // 128) + \
+        4 * sum_m
+    launches = [Launch('contiguous_unfused', mk_c_unfused, 2 * total * n * k, c_bytes),
+                Launch('contiguous_fused', mk_c_fused, 2 * total * n * k, c_bytes),
+                Launch('masked_unfused', mk_m_unfused, 2 * sum_m * n * k, m_bytes),
+                Launch('masked_fused', mk_m_fused, 2 * sum_m * n * k, m_bytes)]
+    cfg = {'workload': 'MoE L1 gate/up GEMM + SwiGLU x weight -> FP8, unfused vs fused (config 3 contiguous and '
+                       'config 4 masked, N = 2 x 2048, K = 7168)',
+           'tokens_per_expert': c['ms'], 'm_padded': m_pad, 'masked_m': m['masked_m'].tolist()}
+    return launches, cfg
+
+
 CAST_MK = [(4096, 7168), (4096, 16384), (4096, 1536), (32768, 7168)]
 
 
@@ -510,6 +593,8 @@ def cpu_baseline(workload: str, sample_m: int):
                      'sample': f'M={rows} rows of each (M,K) shape: the oracle\'s numpy per-token cast '
                                f'(single-threaded numpy), {secs:.2f} s per pass (median)'}, **host)
     nk = DENSE_NK if workload in ('dense', 'dense_acc') else [(4096, 7168), (7168, 2048)]
+    if workload == 'moe_l1':   # the gate/up GEMM (the SwiGLU step is not timed on the host)
+        nk = [(4096, 7168)]
     if workload == 'decode':   # config 1 itself: the whole 64-row workload
         nk, sample_m = [(2112, 7168)], 64
     flops, secs = 0, 0.0
@@ -548,10 +633,10 @@ def load_traffic(workload, launches, configs):
 
 MAKERS = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
           'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast,
-          'kgrouped': make_kgrouped, 'decode': make_decode}
+          'kgrouped': make_kgrouped, 'decode': make_decode, 'moe_l1': make_moe_l1}
 # Configurations summarized next to the headline in the default run (per-launch
 # kernel time and roofline fraction; the headline `value` stays config 2).
-EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4', 'kgrouped', 'decode']
+EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4', 'kgrouped', 'decode', 'moe_l1']
 
 
 def t_min_us(flops, nbytes):
@@ -580,7 +665,9 @@ class Workload:
         for i in range(len(self.launches)):
             for r in range(rot):
                 self.fns[i][r]()
-            self.configs.append(deep_gemm.get_last_config())
+            # (a launch of several library calls describes them itself)
+            describe = getattr(self.fns[i][rot - 1], 'config', None)
+            self.configs.append(describe() if describe else deep_gemm.get_last_config())
         torch.cuda.synchronize()
         # HIP graphs (the library records into a capturing stream like any other);
         # replays take the Python launch overhead out of the timed regions.

@@ -510,15 +510,20 @@ def moe_dispatch(x: Tuple[torch.Tensor, torch.Tensor], topk_idx: torch.Tensor, n
 
 def moe_swiglu_apply_weight_to_fp8(x: torch.Tensor, row_weights: Optional[torch.Tensor] = None,
                                    row_layout: Optional[torch.Tensor] = None, clamp_value: Optional[float] = None,
-                                   gran_k: int = 128) -> Tuple[torch.Tensor, torch.Tensor]:
+                                   gran_k: int = 128, out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+                                   ) -> Tuple[torch.Tensor, torch.Tensor]:
     """bf16 [M, 2I] (gate | up, an L1 grouped GEMM's output) -> (e4m3 [M, I], f32 SF
     [M, I/gran_k]) of y = silu(gate) * up * w: the reference's
     swiglu_apply_weight_to_fp8 (third-party/tilelang_ops/swiglu_apply_weight_to_fp8.py)
     with per_token_cast_to_fp8's scale arithmetic, fused in one HBM pass.
-    row_layout (m_indices): rows with a negative entry are written as zeros."""
+    row_layout (m_indices): rows with a negative entry are written as zeros.
+    out: optional preallocated (q, sf)."""
     m, i2 = x.shape
-    q = torch.empty((m, i2 // 2), dtype=torch.float8_e4m3fn, device=x.device)
-    sf = torch.empty((m, i2 // 2 // gran_k), dtype=torch.float32, device=x.device)
+    if out is not None:
+        q, sf = _pair(out, 'out')
+    else:
+        q = torch.empty((m, i2 // 2), dtype=torch.float8_e4m3fn, device=x.device)
+        sf = torch.empty((m, i2 // 2 // gran_k), dtype=torch.float32, device=x.device)
     _check(_lib.dg_moe_swiglu_apply_weight_to_fp8(_ref(_desc(x)), _opt(row_weights), _opt(row_layout),
                                                   float(clamp_value or 0.0), _ref(_desc(q)), _ref(_desc(sf)),
                                                   int(gran_k), _ffi.stream_of(x)))

@@ -86,6 +86,16 @@ def test_dispatch_empty_and_unrouted():
                                               gen.to_dev(idx), e, layout='psum')
     torch.cuda.synchronize()
     assert bool((pos == -1).all()) and bool((gl == 0).all())
+    # int64 ids: 2^32 + e and -2^32 + e are outside [0, E) and stay unrouted (no
+    # narrowing to e first); the oracle compares in int64 the same way
+    idx64 = np.full((5, 2), -1, np.int64)
+    idx64[0, 0], idx64[1, 1], idx64[2, 0], idx64[4, 1] = 2 ** 32 + 1, -(2 ** 32) + 2, 3, 2 ** 33
+    ref = omoe.dispatch(q, sf, idx64, e, 'contiguous', alignment=128)
+    _, _, gl, pos, _ = deep_gemm.moe_dispatch((gen.to_dev(q, torch.float8_e4m3fn), gen.to_dev(sf)),
+                                              torch.from_numpy(idx64).to(DEV), e)
+    torch.cuda.synchronize()
+    assert np.array_equal(pos.cpu().numpy(), ref['pos'])
+    assert int((pos >= 0).sum()) == 1 and int(pos[2, 0]) == 0
 
 
 @pytest.mark.parametrize('gran,clamp', [(128, None), (32, None), (128, 7.0)])
@@ -130,6 +140,24 @@ def test_combine_vs_oracle(weighted, masked):
     out = deep_gemm.moe_combine(yd, gen.to_dev(pos), gen.to_dev(w) if weighted else None)
     torch.cuda.synchronize()
     assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+def test_combine_skips_rows_past_y():
+    """pos entries at or past y's row count (E * max_m for a 3-D y) are skipped, as
+    negative ones are: the result equals the oracle's combine with them set to -1."""
+    t, k, n, rows = 64, 4, 256, 300
+    rng = np.random.default_rng(22)
+    y = oquant.bf16_round(rng.standard_normal((rows, n)).astype(np.float32))
+    pos = rng.integers(-1, rows, size=(t, k)).astype(np.int32)
+    pos[::3, 1] = rows                      # one past the end
+    pos[::5, 2] = rows + 12345              # far past it
+    pos[7, 0] = 2 ** 31 - 1
+    w = rng.random((t, k)).astype(np.float32)
+    ref = omoe.combine(y, np.where(pos >= rows, -1, pos), w)
+    for yd in (torch.from_numpy(y).bfloat16().to(DEV), torch.from_numpy(y).bfloat16().to(DEV).view(3, 100, n)):
+        out = deep_gemm.moe_combine(yd, gen.to_dev(pos), gen.to_dev(w))
+        torch.cuda.synchronize()
+        assert np.array_equal(out.float().cpu().numpy(), ref)
 
 
 def _layer_oracle(q, sf, idx, w, l1, l2):
