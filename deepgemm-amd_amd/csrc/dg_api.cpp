@@ -471,9 +471,32 @@ bool is_ue8m0_path(const Operands& o, const Recipe& r) {
 }
 
 // expected_m: the masked layout's per-group row hint (tile choice only), else -1.
+// Whether a dense call of at most 64 rows (K % 128 == 0, BF16 D, no C) takes the
+// split-K kernel when given a workspace, and its plan. The chunk count fills
+// the CUs with workgroups of 64 columns (at least two chunks). Measured on
+// MI355X against the kernels the call takes without a workspace (tiny-M /
+// streaming; graph replays over 8 rotating buffer sets after a cache flush, us):
+//   64 x 2112 x 7168 13.5 against 22.4, 16 x 2112 x 7168 11.0 against 12.9,
+//   1 x 2112 x 7168 10.8 against 9.4; 64 x 7168 x 16384 38.1 against 62.2,
+//   64 x 16384 x 7168 (two chunks, two rounds) 37.1 against 42.7;
+//   64 x 7168 x 2048 13.1 against 12.6, 1 x 4096 x 4096 11.0 against 7.5.
+// Its two launches cost ~8 us before any work, so it pays where the single
+// launch is slow: more than 8 rows and K >= 6144 (the variant-10 override
+// takes it anywhere, with block_n chunks or the heuristic's count).
+bool splitk_choice(int64_t m, int64_t n, int64_t k, int cus, SplitKPlan& pl) {
+    const int tv = g_tile_variant.load();
+    const int64_t tiles = ceil_div(n, kSplitKCols);
+    int want = tv == 10 ? g_tile_n.load() : 0;
+    if (tv != 10 && tiles <= cus) want = (int)std::max<int64_t>(2, cus / tiles);
+    pl = plan_fp8_splitk(m, n, k, cus, want);
+    if (tv == 10) return true;
+    return m > 8 && k >= 6144 && tiles <= cus && pl.splits >= 2;
+}
+
+// ws / ws_bytes: a caller-provided device workspace (dense split-K), or null.
 void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int64_t n, int64_t k, int64_t groups,
               int disable_ue8m0_cast, int zero_padding, hipStream_t stream, int expected_m = -1,
-              const dg_epilogue* ep = nullptr) {
+              const dg_epilogue* ep = nullptr, void* ws = nullptr, int64_t ws_bytes = 0) {
     // Epilogue classes and alpha exist on the UE8M0 path only, as in the reference
     // (csrc/apis/gemm.hpp:118-119 for its FP32-scale path); the FP8 stage is a BF16 D
     // without C (csrc/jit_kernels/impls/epilogue_class.hpp:81-84).
@@ -521,6 +544,26 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
         try { args.grid_limit = num_sms_now(); } catch (const Error&) {}
         const int64_t m_rows = m;
         const int tv = g_tile_variant.load();
+        // Dense calls of at most 64 rows with a workspace: K split over workgroups
+        // whenever that gives at least two chunks (variant 10 forces it, block_n
+        // = chunks or 0 for the heuristic's count).
+        if (kind == kNormal && (tv == 0 || tv == 10) && fp8_splitk_supported(args)) {
+            SplitKPlan pl{};
+            const bool chosen = splitk_choice(m_rows, n, k, args.grid_limit, pl);
+            const bool fits = ws != nullptr && ws_bytes >= pl.workspace_bytes;
+            if (tv == 10 && !fits)
+                DG_UNSUPPORTED("tile override: the split-K kernel needs a workspace of "
+                               "dg_fp8_gemm_nt_workspace_size bytes (dg_fp8_fp4_gemm_nt_ws)");
+            if (fits && chosen) {
+                record_config("fp8_gemm_1d2d", kind, TileConfig{pl.rows, kSplitKCols, 10}, m, n, k, groups);
+                t_last_config += " splits=" + std::to_string(pl.splits) + "x" + std::to_string(pl.kper);
+                launch_fp8_gemm_splitk(args, pl, static_cast<float*>(ws), stream);
+                return;
+            }
+        } else if (tv == 10) {
+            DG_UNSUPPORTED("tile override: the split-K kernel runs dense calls of at most 64 rows with K % 128 == 0, "
+                           "BF16 D and no C");
+        }
         TileConfig t;
         // Dense calls of at most kDenseStreamRows rows are weight-stream bound: they
         // run on the streaming kernel as one group (layout null), which loads only
@@ -714,7 +757,7 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
 
 void gemm_nt_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
                   const dg_tensor* d_, const dg_tensor* c, const dg_recipe* recipe, int disable_ue8m0_cast,
-                  const dg_epilogue* ep, hipStream_t stream) {
+                  const dg_epilogue* ep, hipStream_t stream, const dg_tensor* ws_ = nullptr) {
     const View a = view(a_, "a"), sfa = view(sfa_, "sfa"), b = view(b_, "b"), sfb = view(sfb_, "sfb"),
                d = view(d_, "d");
     // Shape must be [M, K] @ [N, K].T; the gfx950 kernels need K-major operands
@@ -732,7 +775,29 @@ void gemm_nt_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b
     const Recipe r = resolve_recipe(recipe, sfa, sfb);
     check_sf_layout(sfa, m, k, r.gran_mn_a, r.gran_k_a, -1);
     check_sf_layout(sfb, n, k, r.gran_mn_b, r.gran_k_b, -1);
-    run_gemm(kNormal, Operands{a, sfa, b, sfb, d, c, nullptr}, r, m, n, k, 1, disable_ue8m0_cast, 0, stream, -1, ep);
+    void* ws = nullptr;
+    int64_t ws_bytes = 0;
+    if (ws_) {
+        const View w = view(ws_, "workspace");
+        DG_CHECK(w.on_device() && w.dim() == 1 && (w.size(0) <= 1 || w.stride(0) == 1));
+        ws = const_cast<void*>(w.data());
+        ws_bytes = w.size(0) * elem_size(w.dtype());
+        DG_CHECK(reinterpret_cast<uintptr_t>(ws) % 16 == 0);
+    }
+    run_gemm(kNormal, Operands{a, sfa, b, sfb, d, c, nullptr}, r, m, n, k, 1, disable_ue8m0_cast, 0, stream, -1, ep,
+             ws, ws_bytes);
+}
+
+// Bytes of the workspace dg_fp8_fp4_gemm_nt_ws uses for an m x n x k call on the
+// FP32-scale path with a BF16 D and no C (0: the call takes no workspace).
+int64_t dense_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || m > kSplitKMaxRows || k % 128 != 0) return 0;
+    int cus = 256;
+    try { cus = num_sms_now(); } catch (const Error&) {}
+    const int tv = g_tile_variant.load();
+    if (tv != 0 && tv != 10) return 0;
+    SplitKPlan pl{};
+    return splitk_choice(m, n, k, cus, pl) ? pl.workspace_bytes : 0;
 }
 
 void contiguous_impl(const dg_tensor* a_, const dg_tensor* sfa_, const dg_tensor* b_, const dg_tensor* sfb_,
@@ -1347,6 +1412,21 @@ int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor
     });
 }
 
+int dg_fp8_fp4_gemm_nt_ws(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b, const dg_tensor* sfb,
+                          const dg_tensor* d, const dg_tensor* c, const dg_recipe* recipe, int32_t disable_ue8m0_cast,
+                          const dg_epilogue* epilogue, const dg_tensor* workspace, void* stream) {
+    return guarded([&] {
+        gemm_nt_impl(a, sfa, b, sfb, d, c, recipe, disable_ue8m0_cast, epilogue, static_cast<hipStream_t>(stream),
+                     workspace);
+    });
+}
+
+int64_t dg_fp8_gemm_nt_workspace_size(int64_t m, int64_t n, int64_t k) {
+    int64_t out = -1;
+    if (guarded([&] { out = dense_workspace_bytes(m, n, k); }) != DG_OK) return -1;
+    return out;
+}
+
 int dg_m_grouped_fp8_fp4_gemm_nt_contiguous(const dg_tensor* a, const dg_tensor* sfa, const dg_tensor* b,
                                             const dg_tensor* sfb, const dg_tensor* d, const dg_tensor* grouped_layout,
                                             const dg_recipe* recipe, int32_t disable_ue8m0_cast,
@@ -1545,6 +1625,7 @@ int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n) {
                         : variant == 8 || variant == 9
                             ? ((block_m == 16 || block_m == 32 || block_m == kTinyMRows) &&
                                (block_n == 16 || block_n == 32 || block_n == 64))
+                        : variant == 10 ? (block_m == 0 && block_n >= 0 && block_n <= 1024)
                                        : (variant == 4 && block_m == 256 && block_n == 256);
         if (!ok) DG_UNSUPPORTED("tile shape not compiled");
         g_tile_m = block_m, g_tile_n = block_n;

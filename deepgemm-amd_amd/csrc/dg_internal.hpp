@@ -109,6 +109,21 @@ constexpr int kTinyMRows = 64;
 bool fp8_tinym_supported(const Fp8GemmArgs& a);
 void launch_fp8_gemm_tinym(const Fp8GemmArgs& a, int waves, int cols, int rows, hipStream_t stream);
 
+// Dense calls of at most 64 rows with K split over workgroups
+// (dg_gemm_fp8_splitk.hip): 64 columns x a chunk of K blocks per workgroup,
+// FP32 partials in a caller-provided workspace, then a reduction in chunk order.
+constexpr int kSplitKCols = 64;
+constexpr int kSplitKMaxRows = 64;
+constexpr int kSplitKMaxChunk = 64;   // K blocks per workgroup at most
+struct SplitKPlan {
+    int splits, kper, rows, tiles;
+    int64_t workspace_bytes;   // tiles x splits x rows x 64 FP32 partials
+};
+bool fp8_splitk_supported(const Fp8GemmArgs& a);
+// splits <= 0: enough chunks to give every CU a workgroup (cus / column slices)
+SplitKPlan plan_fp8_splitk(int64_t m, int64_t n, int64_t k, int cus, int splits);
+void launch_fp8_gemm_splitk(const Fp8GemmArgs& a, const SplitKPlan& plan, float* ws, hipStream_t stream);
+
 // Launch the FP32-scale FP8 GEMM for `kind` with tile `cfg` on `stream`.
 // Throws dgm::Error on unsupported configurations or launch failures.
 void launch_fp8_gemm_1d2d(GemmKind kind, const TileConfig& cfg, const Fp8GemmArgs& args,

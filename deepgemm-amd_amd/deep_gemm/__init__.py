@@ -215,8 +215,19 @@ def fp8_fp4_gemm_nt(a: Tuple[torch.Tensor, torch.Tensor], b: Tuple[torch.Tensor,
 
     def run(out):
         dd = _desc(out)
-        _check(_lib.dg_fp8_fp4_gemm_nt(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dc), _ref(r),
-                                       int(bool(disable_ue8m0_cast)), _ref(ep), _ffi.stream_of(out)))
+        # Decode-sized calls (at most 64 rows) split K over workgroups when given a
+        # workspace: it comes from torch's caching allocator on the output's stream.
+        ws_bytes = 0
+        if c is None and a_t.dim() == 2 and a_t.shape[0] <= 64 and out.dtype == torch.bfloat16:
+            ws_bytes = int(_lib.dg_fp8_gemm_nt_workspace_size(a_t.shape[0], b_t.shape[0], a_t.shape[1]))
+        if ws_bytes > 0:
+            ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=out.device)
+            _check(_lib.dg_fp8_fp4_gemm_nt_ws(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dc), _ref(r),
+                                              int(bool(disable_ue8m0_cast)), _ref(ep), _ref(_desc(ws)),
+                                              _ffi.stream_of(out)))
+        else:
+            _check(_lib.dg_fp8_fp4_gemm_nt(_ref(da), _ref(dsa), _ref(db), _ref(dsb), _ref(dd), _ref(dc), _ref(r),
+                                           int(bool(disable_ue8m0_cast)), _ref(ep), _ffi.stream_of(out)))
     if fp8q is not None:
         _fp8_quantized_output(d, c, a_t.shape[-1], fp8q, run)
     else:
@@ -409,8 +420,10 @@ def transform_sf_into_required_layout(sf: torch.Tensor, mn: int, k: int, recipe,
 # ------------------------------------------------------------------ introspection
 
 def set_tile_override(block_m: int = 0, block_n: int = 0, variant: int = 2) -> None:
-    """Force the FP32-scale kernel variant and tile ((0, 0) = heuristic). Testing/tuning aid."""
-    if block_m == 0 and block_n == 0:
+    """Force the FP32-scale kernel variant and tile ((0, 0) = heuristic; variant 10,
+    the split-K kernel, takes block_m 0 and block_n = K chunks, 0 = its own count).
+    Testing/tuning aid."""
+    if block_m == 0 and block_n == 0 and variant != 10:
         variant = 0
     _check(_lib.dg_set_tile_override(int(variant), int(block_m), int(block_n)))
 

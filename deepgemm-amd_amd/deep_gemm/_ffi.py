@@ -75,6 +75,8 @@ SIGNATURES = {
     'dg_init': (_I, []),
     'dg_shutdown': (_I, []),
     'dg_fp8_fp4_gemm_nt': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _E, _V]),
+    'dg_fp8_fp4_gemm_nt_ws': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _E, _T, _V]),
+    'dg_fp8_gemm_nt_workspace_size': (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     'dg_m_grouped_fp8_fp4_gemm_nt_contiguous': (_I, [_T, _T, _T, _T, _T, _T, _R, _I, _I, _I, _I, _E, _V]),
     'dg_m_grouped_fp8_fp4_gemm_nt_masked': (_I, [_T, _T, _T, _T, _T, _T, _I, _R, _I, _E, _V]),
     'dg_get_tma_aligned_size': (_I, [_I, _I, _P(_I)]),

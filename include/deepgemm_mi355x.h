@@ -136,6 +136,28 @@ int dg_fp8_fp4_gemm_nt(const dg_tensor* a, const dg_tensor* sfa,
                        const dg_epilogue* epilogue,
                        void* stream);
 
+/* dg_fp8_fp4_gemm_nt with a caller-provided device workspace. The reference's
+ * fp8_gemm_nt takes none (csrc/apis/gemm.hpp:78-133); this variant lets dense
+ * calls of at most 64 rows (decode; K % 128 == 0, FP32 scales, BF16 D, no C) split
+ * K over workgroups: FP32 partial tiles go to the workspace and a second kernel
+ * adds them in a fixed order (deterministic). `workspace` is a 1-D device tensor
+ * of at least dg_fp8_gemm_nt_workspace_size(M, N, K) bytes, 16-byte aligned,
+ * used only until the call's kernels finish on `stream` (stream-ordered; the
+ * caller may reuse it for the next call on the same stream). NULL, or one too
+ * small, gives exactly dg_fp8_fp4_gemm_nt. */
+int dg_fp8_fp4_gemm_nt_ws(const dg_tensor* a, const dg_tensor* sfa,
+                          const dg_tensor* b, const dg_tensor* sfb,
+                          const dg_tensor* d, const dg_tensor* c,
+                          const dg_recipe* recipe,
+                          int32_t disable_ue8m0_cast,
+                          const dg_epilogue* epilogue,
+                          const dg_tensor* workspace,
+                          void* stream);
+
+/* Workspace bytes dg_fp8_fp4_gemm_nt_ws uses for an M x N x K call (0: the call
+ * runs without one; -1 on error). No reference counterpart. */
+int64_t dg_fp8_gemm_nt_workspace_size(int64_t m, int64_t n, int64_t k);
+
 /* M-grouped contiguous GEMM (prefill MoE).
  * Replaces m_grouped_fp8_fp4_gemm_nt_contiguous / m_grouped_fp8_gemm_nt_contiguous
  * (csrc/apis/gemm.hpp:181-250, registered :870-879, aliases :926-927).
@@ -396,7 +418,9 @@ int32_t dg_get_theoretical_mk_alignment_for_contiguous_layout(int32_t expected_m
  * over the tile sequence like the reference's scheduler; 256 x 256 only),
  * 5 = the weight-streaming kernel (block_m 16 or 160 rows per pass), 6 / 7 =
  * the 1D1D kernels, 8 / 9 = the tiny-M kernel with 8 / 4 waves (block_m = rows
- * per workgroup, 16, 32 or 64; block_n = columns per workgroup, 16, 32 or 64);
+ * per workgroup, 16, 32 or 64; block_n = columns per workgroup, 16, 32 or 64),
+ * 10 = the split-K kernel of dg_fp8_fp4_gemm_nt_ws (block_m 0; block_n = K
+ * chunks, 0 for the heuristic's count);
  * variant 0 restores the heuristic. Only compiled tile shapes are accepted. */
 int dg_set_tile_override(int32_t variant, int32_t block_m, int32_t block_n);
 

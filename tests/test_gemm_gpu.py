@@ -607,6 +607,8 @@ def test_dense_tiny_m_split_k_kernel(m, n, k):
         print(f'  {cfg}', flush=True)
         if v:
             assert f' v{v} ' in cfg and f'block_m={rows} block_n={bn} ' in cfg, cfg
+        elif 8 < m <= 64 and k >= 6144 and (n + 63) // 64 <= 256:
+            assert ' v10 ' in cfg, cfg   # the split-K kernel (below) takes these by default
         elif n <= 7168:
             assert ' v8 ' in cfg or ' v9 ' in cfg, cfg
         out = d.float().cpu().numpy()
@@ -617,6 +619,105 @@ def test_dense_tiny_m_split_k_kernel(m, n, k):
         if v:   # a row tile's arithmetic does not depend on how the rows are split
             first = by_cfg.setdefault((v, bn), d)
             assert torch.equal(first.view(torch.int16), d.view(torch.int16)), f'rows {rows} differ'
+
+
+@pytest.mark.parametrize('m,n,k', [(64, 2112, 7168), (1, 2112, 7168), (16, 7168, 2048), (33, 4096, 7168),
+                                   (7, 576, 7168), (3, 104, 384), (50, 138, 1024), (64, 7168, 16384),
+                                   (17, 4096, 4096), (1, 24576, 1536), (64, 64, 32768)])
+def test_dense_split_k_kernel(m, n, k):
+    """The split-K kernel (64 columns x a chunk of K blocks per workgroup, FP32
+    partials in a workspace, added in chunk order by a second kernel): the oracle
+    within one BF16 ulp plus 2^-15 x sum |a b| for the heuristic's chunk count and
+    forced counts (1, 3, 8, one chunk per K block), ragged M and N (104; 138 in a
+    D whose rows are padded to 144, so the last 4-column group is partial),
+    MN-major SFA equal to K-major, bitwise-identical reruns. The default routing
+    (a workspace from torch) takes it for M <= 64 when it gives at least two
+    chunks, more than 8 rows and K >= 6144; config 1 (64 x 2112 x 7168) is one of these."""
+    x = gen.dense_inputs(m, n, k, seed=190 + m + n)
+    a_deq, b_deq = oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb'])
+    ref = ogemm.gemm_nt(a_deq, b_deq)
+    s_abs = ogemm.gemm_nt(np.abs(a_deq), np.abs(b_deq))
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    sfa_mn = deep_gemm.get_mn_major_tma_aligned_tensor(a[1])
+    tol = np.abs(ref) * 2.0 ** -8 + 2.0 ** -15 * s_abs
+    nkb = k // 128
+    pitch = (n + 7) // 8 * 8   # 16-byte rows
+
+    full = {}
+
+    def out_d():
+        full['d'] = sentinel_bf16((m, pitch))
+        return full['d'][:, :n]
+    for splits in (0, 1, 3, 8, nkb):
+        if splits > nkb:
+            continue
+        deep_gemm.set_tile_override(0, splits, variant=10)
+        try:
+            d2, d3 = out_d(), out_d()
+            d = out_d()
+            deep_gemm.fp8_gemm_nt(a, b, d)
+            cfg = deep_gemm.get_last_config()
+            deep_gemm.fp8_gemm_nt((a[0], sfa_mn), b, d2)
+            for _ in range(3):
+                deep_gemm.fp8_gemm_nt(a, b, d3)
+        finally:
+            deep_gemm.set_tile_override(0, 0)
+        torch.cuda.synchronize()
+        print(f'  {cfg}', flush=True)
+        assert ' v10 ' in cfg, cfg
+        out = d.float().cpu().numpy()
+        diff, _ = report(f'dense split-K M={m} N={n} K={k} [{cfg.split("groups=1 ")[-1]}]', out, ref)
+        assert diff < 1e-3
+        assert np.all(np.abs(out - ref) <= tol)
+        assert torch.equal(d2.view(torch.int16), d.view(torch.int16))
+        assert torch.equal(d3.view(torch.int16), d.view(torch.int16))
+        if pitch > n:   # the padding columns of D stay untouched
+            assert bool((full['d'][:, n:].view(torch.int16) == SENTINEL).all())
+    d = out_d()
+    deep_gemm.fp8_gemm_nt(a, b, d)
+    cfg = deep_gemm.get_last_config()
+    torch.cuda.synchronize()
+    if m > 8 and k >= 6144 and (n + 63) // 64 <= 256:
+        assert ' v10 ' in cfg, cfg
+    else:
+        assert ' v10 ' not in cfg, cfg
+    assert np.all(np.abs(d.float().cpu().numpy() - ref) <= tol)
+
+
+def test_dense_split_k_workspace_rules():
+    """The workspace entry point: the size query matches what a call needs, a
+    workspace one byte short runs the workspace-free kernels instead (same
+    oracle bound), and the plain entry point never takes the split-K path."""
+    m, n, k = 64, 2112, 7168
+    lib = deep_gemm._ffi.lib
+    need = lib.dg_fp8_gemm_nt_workspace_size(m, n, k)
+    assert need == 33 * 7 * 64 * 64 * 4, need   # FP32 partials: column slices x chunks x rows x 64
+    assert lib.dg_fp8_gemm_nt_workspace_size(65, n, k) == 0       # more than 64 rows
+    assert lib.dg_fp8_gemm_nt_workspace_size(8, n, k) == 0        # 8 rows: the single-launch kernels win
+    assert lib.dg_fp8_gemm_nt_workspace_size(m, n, 4096) == 0     # K < 6144 likewise
+    assert lib.dg_fp8_gemm_nt_workspace_size(m, n, 7168 + 64) == 0  # K tail
+    assert lib.dg_fp8_gemm_nt_workspace_size(m, 24576, 1536) == 0   # one chunk per CU already
+    x = gen.dense_inputs(m, n, k, seed=201)
+    ref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    from deep_gemm._ffi import describe, ref as cref
+    outs = []
+    for nbytes, entry in ((need, 'ws'), (need - 16, 'ws'), (0, 'plain')):
+        d = sentinel_bf16((m, n))
+        dd = describe(d)
+        args = [cref(describe(t)) for t in (a[0], a[1], b[0], b[1])] + [cref(dd), None, None, 0, None]
+        if entry == 'ws':
+            ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=DEV)
+            st = lib.dg_fp8_fp4_gemm_nt_ws(*args, cref(describe(ws)), deep_gemm._ffi.stream_of(d))
+        else:
+            st = lib.dg_fp8_fp4_gemm_nt(*args, deep_gemm._ffi.stream_of(d))
+        assert st == 0, lib.dg_last_error()
+        outs.append((deep_gemm.get_last_config(), d))
+    torch.cuda.synchronize()
+    assert ' v10 ' in outs[0][0] and ' v10 ' not in outs[1][0] and ' v10 ' not in outs[2][0], [o[0] for o in outs]
+    assert torch.equal(outs[1][1].view(torch.int16), outs[2][1].view(torch.int16))
+    for _, d in outs:
+        assert ogemm.calc_diff(d.float().cpu().numpy(), ref) < 1e-3
 
 
 def test_dense_tiny_m_k_bound():
