@@ -310,14 +310,20 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     const int tv = g_tile_variant.load(), tm = g_tile_m.load(), tn = g_tile_n.load();
     // The pipelined kernel keeps one SFB value per K block in LDS (up to 1024 blocks).
     const bool pipe_ok = ceil_div(k, 128) <= 1024;
+    // The 256 x 256 pipelined tile is not built for K % 128 != 0 (its K-tail
+    // schedule spills registers); the other tiles give the same bits.
+    const bool tile256_ok = k % 128 == 0;
     if (tv == 4) {   // persistent form of the pipelined kernel
         if (!pipe_ok || tm != 256 || tn != 256) DG_UNSUPPORTED("tile override: the persistent kernel is 256 x 256");
+        if (!tile256_ok) DG_UNSUPPORTED("tile override: the 256 x 256 pipelined tile needs K % 128 == 0");
         if (!grouped_tile_ok(kind, tv, tm, align_m)) DG_UNSUPPORTED("tile override block_m does not fit the M alignment");
         return {256, 256, 4};
     }
     if (tv > 0) {
         const bool ok = tv == 1 ? fp8_1d2d_tile_supported(tm, tn) : (pipe_ok && fp8_1d2d_v2_tile_supported(tm, tn));
         if (!ok) DG_UNSUPPORTED("tile override not compiled");
+        if (tv == 2 && tm == 256 && tn == 256 && !tile256_ok)
+            DG_UNSUPPORTED("tile override: the 256 x 256 pipelined tile needs K % 128 == 0");
         if (!grouped_tile_ok(kind, tv, tm, align_m))
             DG_UNSUPPORTED("tile override block_m does not fit the M alignment");
         return {tm, tn, tv};
@@ -336,10 +342,8 @@ TileConfig choose_tile_1d2d(GemmKind kind, int64_t m_rows, int64_t n, int64_t k,
     for (const auto& c : cands) {
         if (!grouped_tile_ok(kind, c.variant, c.bm, align_m)) continue;
         if (c.variant == 2 && !pipe_ok) continue;
-        // K % 128 != 0: the 256 x 256 pipelined tile's K-tail schedule (per-lane
-        // 64-bit load addresses next to 256 registers of accumulators) spills to
-        // scratch; the other tiles' K-tail schedules do not.
-        if (c.variant == 2 && c.bm == 256 && c.bn == 256 && k % 128 != 0) continue;
+        // K % 128 != 0: the 256 x 256 pipelined tile has no K-tail schedule.
+        if (c.variant == 2 && c.bm == 256 && c.bn == 256 && !tile256_ok) continue;
         const int64_t tiles = ceil_div(m_rows, c.bm) * ceil_div(n, c.bn) * groups;
         const int64_t slots = (int64_t)cus * c.per_cu;
         const double rounds = (double)ceil_div(tiles, slots);

@@ -758,11 +758,18 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     constexpr bool KSA_OK = STAGES == 2 && !PERSIST && (KIND == kNormal || KIND == kContiguous);
     const bool kmajor = KSA_OK && a.sfa_sk == 1 && a.sfa_sm % 4 == 0 && (reinterpret_cast<uintptr_t>(a.sfa) & 15) == 0;
     const int ksa = !kmajor || a.k > kMaxKBlocksKsa * kBK ? 0 : a.k % (4 * kBK) == 0 ? 4 : 0;
+    // The K-tail schedule of the 256 x 256 tile (per-lane 64-bit load addresses next
+    // to 256 registers of accumulators) spills to scratch: it is not built, and
+    // the host never routes a K tail to this tile (K-tail calls take 256 x 192 or
+    // smaller tiles, which compute the same bits).
+    constexpr bool KT_OK = !(BM == 256 && BN == 256);
+    if (k_tail && !KT_OK) DG_UNSUPPORTED("the 256 x 256 pipelined tile needs K % 128 == 0");
 #define DG_PIPE_LAUNCH(OF, HC)                                                                                       \
     do {                                                                                                             \
         if (k_tail)                                                                                                  \
-            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 1, PERSIST>), gdim, \
-                               bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
+            hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, KT_OK ? 1 : 0,      \
+                                                          PERSIST>),                                                 \
+                               gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                    \
         else if (ksa == 4)                                                                                           \
             hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, OF, HC, 0, PERSIST, 0,        \
                                                           KSA_OK ? 4 : 0>),                                          \
@@ -774,7 +781,8 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
     if (a.sw_q) {   // fused SwiGLU -> FP8 epilogue (m-grouped 256-column tiles)
         if constexpr (BN == 256 && !PERSIST && (KIND == kContiguous || KIND == kMasked || KIND == kPsum)) {
             if (k_tail)
-                hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 1, 0, 0, 0, 1>),
+                hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, KT_OK ? 1 : 0, 0, 0,
+                                                              0, 1>),
                                    gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
             else if (ksa == 4)
                 hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 0, 0, 0,

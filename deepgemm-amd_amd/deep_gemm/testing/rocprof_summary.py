@@ -71,10 +71,31 @@ def phase_slices(num_launches: int, steps: int, rot: int, disp=None):
     return out, per
 
 
+MAX_CLOCK_GHZ = 2.4   # MI355X's highest shader clock
+
+
+def mfma_utilization(busy_cycles: float, gui_cycles: float, kernel_us: float, simds: int) -> dict:
+    """MFMA busy fraction of one call from its counters: busy cycles summed over
+    the SIMDs, GRBM_GUI_ACTIVE (GPU-busy clocks, per XCD) of the counter run, and
+    the kernel's duration from the trace run. GRBM_GUI_ACTIVE over the traced
+    duration is the clock; when that exceeds the chip's 2.4 GHz maximum, the
+    counter also counted time outside the kernel (short launches under the
+    counter run), so the kernel's clocks are taken as duration x 2.4 GHz instead
+    (a lower bound on the busy fraction) and the entry is flagged."""
+    clock = gui_cycles / (kernel_us * 1e3)
+    over = clock > MAX_CLOCK_GHZ
+    cyc = kernel_us * 1e3 * MAX_CLOCK_GHZ if over else gui_cycles
+    return {'mfma_busy_frac': busy_cycles / (cyc * simds), 'clock_ghz': min(clock, MAX_CLOCK_GHZ),
+            'clock_capped': 1 if over else 0, 'gui_clock_ghz': clock}
+
+
 def dispatches_per_call(config: str) -> int:
-    """Kernels one library call dispatches: a dense column split or a contiguous
-    row split runs two."""
-    return 2 if ('split_n=' in config or 'split_m=' in config) else 1
+    """Kernels one bench launch dispatches: a dense column split, a contiguous row
+    split or the split-K kernel (partials, then the reduction) runs two; a launch
+    of several library calls (configs joined by ' + ') sums them."""
+    if ' + ' in config:
+        return sum(dispatches_per_call(c) for c in config.split(' + '))
+    return 2 if ('split_n=' in config or 'split_m=' in config or ' splits=' in config) else 1
 
 
 def _workgroups(row) -> int:
@@ -187,7 +208,7 @@ def summarize(args):
         for name, sl, p, d in zip(names, psl, per, disp):
             b = sum(bseq[i][2] for i in sl) / (len(sl) / d)   # per call
             cyc = sum(gseq2[i][2] for i in sl) / (len(sl) / d) / args.xcds
-            mfma[name] = {'mfma_busy_frac': b / (cyc * args.simds), 'clock_ghz': cyc / (p['avg_us'] * 1e3)}
+            mfma[name] = mfma_utilization(b, cyc, p['avg_us'], args.simds)
 
     lines = []
     lines.append(f"# {bench['config']['workload']}\n")
@@ -232,11 +253,14 @@ def summarize(args):
     if mfma:
         lines.append('## MFMA utilization (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs))\n')
         lines.append(f'{args.simds} SIMDs, GRBM_GUI_ACTIVE averaged over {args.xcds} XCDs; the clock is '
-                     'GRBM_GUI_ACTIVE over the traced kernel time (under the counter run, so approximate).\n')
+                     'GRBM_GUI_ACTIVE over the traced kernel time (under the counter run, so approximate). '
+                     'Where that exceeds 2.4 GHz (marked *), GRBM_GUI_ACTIVE counted time outside the kernel: '
+                     'the clock is taken as 2.4 GHz and MFMA busy is a lower bound.\n')
         lines.append('| launch | MFMA busy | clock GHz | MFMA busy x clock / 2.4 GHz |')
         lines.append('|---|---|---|---|')
         for n, v in mfma.items():
-            lines.append(f"| {n} | {100 * v['mfma_busy_frac']:.1f}% | {v['clock_ghz']:.2f} | "
+            mark = f" * (GRBM {v['gui_clock_ghz']:.2f})" if v['clock_capped'] else ''
+            lines.append(f"| {n} | {100 * v['mfma_busy_frac']:.1f}% | {v['clock_ghz']:.2f}{mark} | "
                          f"{100 * v['mfma_busy_frac'] * v['clock_ghz'] / 2.4:.1f}% |")
         lines.append('')
     os.makedirs(os.path.dirname(os.path.abspath(args.md)), exist_ok=True)

@@ -95,11 +95,13 @@ def to_dev(x: np.ndarray, dtype=None, device='cuda'):
 
 
 def dense_call_same_order(deep_gemm, a, b, d):
-    """fp8_gemm_nt on the pipelined 256 x 256 tile, whose MFMA pair and per-K-block
-    promotion order every grouped kernel shares, so a contiguous segment or a masked
-    expert must equal it bit for bit. (By default a dense call of at most 16 rows
-    takes the tiny-M kernel, which groups the K sum differently.)"""
-    deep_gemm.set_tile_override(256, 256, variant=2)
+    """fp8_gemm_nt on the pipelined 256 x 256 tile (256 x 192 when K % 128 != 0, which
+    has no 256 x 256 schedule; every pipelined tile gives the same bits), whose MFMA
+    pair and per-K-block promotion order every grouped kernel shares, so a
+    contiguous segment or a masked expert must equal it bit for bit. (By default a
+    dense call of at most 64 rows takes the tiny-M or split-K kernels, which group
+    the K sum differently.)"""
+    deep_gemm.set_tile_override(256, 256 if a[0].shape[-1] % 128 == 0 else 192, variant=2)
     try:
         deep_gemm.fp8_gemm_nt(a, b, d)
     finally:

@@ -249,6 +249,22 @@ def test_grouped_validation():
     assert st == _ffi.DG_ERR_INVALID and 'expected_m > 0' in _ffi.lib.dg_last_error().decode()
 
 
+def test_k_tail_rejects_256x256_override():
+    """The 256 x 256 pipelined tile has no K-tail schedule (it would spill
+    registers): a tile override that would launch it with K % 128 != 0 (plain
+    or persistent) is refused on the host, before any launch."""
+    a, sfa, b, sfb, d = good_dense(512, 512, 1040)
+    sfa = fake((512, 9), _ffi.DG_F32)
+    sfb = fake((4, 9), _ffi.DG_F32)
+    for variant in (2, 4):
+        deep_gemm.set_tile_override(256, 256, variant=variant)
+        try:
+            st, msg = call_nt(a, sfa, b, sfb, d)
+        finally:
+            deep_gemm.set_tile_override(0, 0)
+        assert st == _ffi.DG_ERR_UNSUPPORTED and 'K % 128 == 0' in msg, (variant, msg)
+
+
 def test_fused_swiglu_host_checks():
     """dg_m_grouped_fp8_gemm_nt_{contiguous,masked}_swiglu: shape, dtype and layout
     checks run on the host before any launch."""

@@ -82,3 +82,24 @@ def test_dispatches_per_call():
     assert rs.dispatches_per_call('fp8_gemm_1d2d v2 kind=normal block_m=256 block_n=256 split_n=4096:256x192') == 2
     assert rs.dispatches_per_call('fp8_gemm_1d2d v2 kind=m_grouped_contiguous block_m=256 block_n=256 '
                                   'split_m=32768:128x128') == 2
+
+
+def test_dispatches_per_call_split_k_and_joined_calls():
+    assert rs.dispatches_per_call('fp8_gemm_1d2d v10 kind=normal block_m=64 block_n=64 m=64 n=2112 k=7168 '
+                                  'groups=1 splits=7x8') == 2
+    assert rs.dispatches_per_call('fp8_gemm_1d2d v2 kind=m_grouped_contiguous block_m=256 block_n=256 + '
+                                  'moe_swiglu_cast gran_k=128 m=33408 n=2048') == 2
+
+
+def test_mfma_clock_capped_at_chip_maximum():
+    """GRBM_GUI_ACTIVE over the traced duration gives the clock; above 2.4 GHz the
+    counter included time outside the kernel, so the busy fraction is taken over
+    duration x 2.4 GHz (a lower bound) and flagged; below it is used as is."""
+    simds = 1024
+    # 10 us kernel, 2.0 GHz: 20000 cycles; half of them MFMA-busy on every SIMD
+    v = rs.mfma_utilization(0.5 * 20000 * simds, 20000, 10.0, simds)
+    assert abs(v['mfma_busy_frac'] - 0.5) < 1e-12 and abs(v['clock_ghz'] - 2.0) < 1e-12 and not v['clock_capped']
+    # 10 us kernel whose GRBM count implies 3.28 GHz: capped at 2.4 GHz
+    v = rs.mfma_utilization(0.5 * 24000 * simds, 32800, 10.0, simds)
+    assert v['clock_capped'] and abs(v['clock_ghz'] - 2.4) < 1e-12 and abs(v['gui_clock_ghz'] - 3.28) < 1e-12
+    assert abs(v['mfma_busy_frac'] - 0.5) < 1e-12
