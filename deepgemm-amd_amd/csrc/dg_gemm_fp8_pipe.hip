@@ -229,16 +229,25 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const float* __restrict__ sb_base = p.sfb + (int64_t)expert * p.sfb_gs + (k_off / kBK) * p.sfb_sk +
                                         (int64_t)n0 * p.sfb_sn;
     if (pass > 0) __syncthreads();   // every wave is done with the stage ring and s_sfb of the previous pass
+    // The tile's SFB rows (at most two 128-row groups) straight into LDS, 64 K
+    // blocks per wave load, ahead of the stage loads: the first stage wait (vector
+    // loads retire in order) and its barrier cover them, so their latency overlaps
+    // the first stages' instead of preceding it. (Loaded through registers, a
+    // barrier had to separate them from the stage loads: config-2 step 869-876
+    // against 879-881 us, interleaved runs.)
     if constexpr (!SB1D) {
         const float* sfb_g = p.sfb + (int64_t)expert * p.sfb_gs;
         const int last_row = (p.n - 1) >> 7;
-        for (int idx = tid; idx < 2 * num_kb; idx += NT) {
-            const int gsel = idx / num_kb, kb = idx % num_kb;
+        const uint32_t sfb_lds =
+            __builtin_amdgcn_readfirstlane(lds_address(reinterpret_cast<const uint8_t*>(&s_sfb[0][0])));
+        const int segs = (num_kb + 63) / 64;
+        for (int i = wave; i < 2 * segs; i += NW) {
+            const int gsel = i / segs, kb = (i % segs) * 64 + lane;
             const int row = min((n0 >> 7) + gsel, last_row);
-            s_sfb[gsel][kb] = sfb_g[(int64_t)row * p.sfb_sn + (int64_t)kb * p.sfb_sk];
+            const float* src = sfb_g + (int64_t)row * p.sfb_sn + (int64_t)min(kb, num_kb - 1) * p.sfb_sk;
+            dma4_vaddr(src, sfb_lds + (uint32_t)(gsel * (int)sizeof(s_sfb[0]) + (i % segs) * 256));
         }
     }
-    __syncthreads();   // s_sfb visible; no stage loads are in flight yet
 
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
