@@ -17,7 +17,10 @@ Other workloads (`--workload`): dense_acc (FP32 C += A.B^T), contiguous
 fp8fp4 (config 5), cast (the fused per-token FP8 activation cast that produces
 A and its MN-major SFA for these GEMMs; HBM-bound, reported in GB/s), kgrouped
 (k_grouped_fp8_gemm_nt_contiguous, the 1D1D weight-gradient GEMM), decode
-(config 1's shape, 64 x 2112 x 7168, on the GPU).
+(config 1's shape, 64 x 2112 x 7168, on the GPU), moe_l1 (the config 3 / 4
+gate-up GEMMs with the fused SwiGLU x weight -> FP8 epilogue, beside the
+unfused GEMM + cast), moe_dispatch (token rows -> the contiguous expert layout,
+256 experts, top-8; HBM-bound, GB/s).
 
 Prints one JSON line. `roofline` is computed from per-launch durations measured
 live with HIP events on the launch stream; `cpu_baseline` times the oracle/
@@ -43,7 +46,8 @@ PROFILE_NAMES = {'dense': 'fp8_gemm_nt_dense_m4096', 'dense_acc': 'fp8_gemm_nt_d
                  'contiguous': 'm_grouped_fp8_gemm_nt_contiguous_e8_t32768',
                  'masked': 'm_grouped_fp8_gemm_nt_masked_e16_m256', 'fp8fp4': 'fp8_fp4_gemm_nt_m4096',
                  'cast': 'per_token_cast_to_fp8_bf16', 'kgrouped': 'k_grouped_fp8_gemm_nt_e8_m4096_n7168',
-                 'decode': 'fp8_gemm_nt_m64_n2112_k7168', 'moe_l1': 'moe_l1_swiglu_e8_t32768_e16_m256'}
+                 'decode': 'fp8_gemm_nt_m64_n2112_k7168', 'moe_l1': 'moe_l1_swiglu_e8_t32768_e16_m256',
+                 'moe_dispatch': 'moe_dispatch_e256_top8'}
 
 
 def parse():
@@ -53,7 +57,7 @@ def parse():
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--workload', default='dense',
                     choices=['dense', 'dense_acc', 'contiguous', 'masked', 'fp8fp4', 'cast', 'kgrouped', 'decode',
-                             'moe_l1'])
+                             'moe_l1', 'moe_dispatch'])
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-extras', action='store_true',
                     help='default workload only: skip the per-launch summaries of the other configurations')
@@ -519,6 +523,40 @@ def make_moe_l1():
     return launches, cfg
 
 
+def make_moe_dispatch():
+    """The MoE dispatch (token-major FP8 rows -> the contiguous expert layout):
+    256 experts, top-8, at a decode-sized 4096 tokens (K = 7168) and at 65536
+    tokens (K = 2048), close to the allocation-free entry point's bound. Bytes:
+    each token row read once (codes and SF row) with its routing ids and weights;
+    each routed row and each padding row (alignment 128) written once (codes, SF
+    row, weight), m_indices over every row of the layout, and pos; no FLOPs."""
+    import numpy as np
+    import torch
+    import deep_gemm
+    dev = torch.device('cuda:0')
+    launches = []
+    for t, kdim in [(4096, 7168), (65536, 2048)]:
+        e, topk = 256, 8
+        rng = np.random.default_rng(t)
+        idx = torch.from_numpy(np.argsort(rng.random((t, e)), axis=1)[:, :topk].astype(np.int32)).to(dev)
+        w = torch.rand((t, topk), generator=torch.Generator().manual_seed(t)).to(dev)
+        x = deep_gemm.per_token_cast_to_fp8(torch.randn((t, kdim), device=dev, dtype=torch.bfloat16), False)
+
+        def mk(x=x, idx=idx, w=w, e=e):
+            x2 = _twin(x)
+            return lambda: deep_gemm.moe_dispatch(x2, idx, e, layout='contiguous', topk_weights=w)
+        sfk = (kdim + 127) // 128
+        align = deep_gemm.get_mk_alignment_for_contiguous_layout()
+        per_expert = np.bincount(idx.cpu().numpy().ravel(), minlength=e)
+        seg_rows = int(((per_expert + align - 1) // align * align).sum())
+        cap = int(deep_gemm._lib.dg_moe_dispatch_max_rows(t, topk, e, align))
+        nbytes = (t * (kdim + 4 * sfk) + t * topk * 8                  # token rows, ids, weights
+                  + seg_rows * (kdim + 4 * sfk + 4) + 4 * cap + 4 * t * topk)   # rows + padding, m_indices, pos
+        launches.append(Launch(f't{t}_k{kdim}_e{e}_top{topk}', mk, 0, nbytes))
+    cfg = {'workload': 'moe_dispatch contiguous layout, 256 experts, top-8', 'tk': [(4096, 7168), (65536, 2048)]}
+    return launches, cfg
+
+
 CAST_MK = [(4096, 7168), (4096, 16384), (4096, 1536), (32768, 7168)]
 
 
@@ -582,6 +620,19 @@ def cpu_baseline(workload: str, sample_m: int):
         blas_threads = None
     host = {'cpu_model': _cpu_model(), 'os_cpu_count': os.cpu_count(), 'affinity_cpus': affinity,
             'torch_threads': torch.get_num_threads(), 'blas_threads': blas_threads, 'timing': 'median of 3 after 1 warm-up'}
+    if workload == 'moe_dispatch':
+        from oracle import moe as omoe
+        t, kdim, e, topk = 8 * sample_m, 2048, 256, 8
+        rng = np.random.default_rng(0)
+        idx = np.argsort(rng.random((t, e)), axis=1)[:, :topk].astype(np.int32)
+        w = rng.random((t, topk)).astype(np.float32)
+        codes = rng.integers(0, 126, (t, kdim)).astype(np.uint8)
+        sf = rng.random((t, kdim // 128)).astype(np.float32)
+        secs = _median_time(lambda: omoe.dispatch(codes, sf, idx, e, 'contiguous', 128, topk_weights=w))
+        nbytes = 2 * t * topk * (kdim + 4 * (kdim // 128) + 4) + t * topk * 8 + 4 * t * topk
+        return dict({'value': round(nbytes / secs / 1e9, 3), 'unit': 'GB/s', 'cores': 1, 'kind': 'port',
+                     'sample': f'T={t} tokens, K={kdim}, 256 experts, top-8: the oracle\'s dispatch (numpy, '
+                               f'single-threaded), {secs:.2f} s per pass (median)'}, **host)
     if workload == 'cast':
         rows = 32 * sample_m   # the cast is far cheaper per row than a GEMM row
         nbytes, secs = 0, 0.0
@@ -633,7 +684,8 @@ def load_traffic(workload, launches, configs):
 
 MAKERS = {'dense': lambda: make_dense(False), 'dense_acc': lambda: make_dense(True),
           'contiguous': make_contiguous, 'masked': make_masked, 'fp8fp4': make_fp8fp4, 'cast': make_cast,
-          'kgrouped': make_kgrouped, 'decode': make_decode, 'moe_l1': make_moe_l1}
+          'kgrouped': make_kgrouped, 'decode': make_decode, 'moe_l1': make_moe_l1,
+          'moe_dispatch': make_moe_dispatch}
 # Configurations summarized next to the headline in the default run (per-launch
 # kernel time and roofline fraction; the headline `value` stays config 2).
 EXTRAS = ['dense_acc', 'contiguous', 'masked', 'fp8fp4', 'kgrouped', 'decode', 'moe_l1']
@@ -784,7 +836,7 @@ def main():
     total_flops = sum(l.flops for l in launches) * args.steps
     total_bytes = sum(l.nbytes for l in launches)
     value = total_flops / elapsed / 1e12
-    cast = args.workload == 'cast'
+    cast = args.workload in ('cast', 'moe_dispatch')
     if cast:   # a byte-moving workload: GB/s
         value = total_bytes * args.steps / elapsed / 1e9
 
@@ -823,7 +875,9 @@ def main():
                 'per_launch_frac': {k: v['frac'] for k, v in summ['per_launch'].items()},
                 'per_launch_bound': {k: v['bound'] for k, v in summ['per_launch'].items()}}
     out = {
-        'metric': ('FP8 per-token activation cast GB/s (bf16 -> e4m3 + 1x128 SFA)' if cast else
+        'metric': ('MoE dispatch GB/s (routed FP8 rows into the contiguous expert layout)'
+                   if args.workload == 'moe_dispatch' else
+                   'FP8 per-token activation cast GB/s (bf16 -> e4m3 + 1x128 SFA)' if cast else
                    'FP8 block-scaled GEMM TFLOPS + % of MI355X FP8 MFMA peak, DSV3 shapes'),
         'value': round(value, 2),
         'unit': 'GB/s' if cast else 'TFLOPS',
@@ -834,7 +888,7 @@ def main():
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
-        'dtype': ('bf16 -> e4m3' if cast else
+        'dtype': ('e4m3 rows' if args.workload == 'moe_dispatch' else 'bf16 -> e4m3' if cast else
                   'e4m3 (fp32 accumulate)' if args.workload != 'fp8fp4' else 'e4m3 x e2m1 (fp32 accumulate)'),
         'data': 'synthetic (seeded randn, bf16 -> quantized)',
         'config': wl.cfg,

@@ -7,17 +7,22 @@
 //
 // Dispatch (all integer work, deterministic): each (token t, slot j) routed to
 // expert e gets the next row of e's segment, in token-then-slot order.
-//   1. count:   per chunk of tokens, LDS counters per expert (order-free sums);
-//   2. scan:    per expert an exclusive prefix over chunks, then the segment
-//               starts (aligned for the contiguous and psum layouts) and the
-//               psum ends / masked counts;
-//   3. pad:     contiguous / psum segment padding rows get zero A, SF and
-//               weight, and m_indices = -1 (also every row past the segments);
-//   4. scatter: per chunk, one wave ranks the chunk's entries among equal
-//               experts with ballots (in entry order), then the workgroup copies
-//               each routed row (K bytes of codes, its SF row, its weight).
-// Bytes: the scatter reads and writes each routed row once (HBM-bound copy);
-// counts and scans touch 4 bytes per entry and per (chunk, expert).
+//   1. count:   per chunk of 64 tokens, one wave ranks the chunk's entries
+//               among equal experts with ballots (in entry order; the rank goes
+//               to pos) and leaves the chunk's count per expert;
+//   2. scan:    one wave per expert: exclusive prefix over chunks, the total,
+//               and the masked counts;
+//   3. starts:  (contiguous / psum) one block scans the aligned totals into
+//               the segment starts and the psum ends;
+//   4. scatter: one wave per token turns its k ranks into rows, reads the
+//               token's K bytes once and stores them to each routed row, with
+//               the SF row, the weight and m_indices; beside them (contiguous /
+//               psum) a block per expert fills its padding rows (zero A, SF and
+//               weight, m_indices = -1), and one more sets m_indices = -1 past
+//               the segments.
+// Bytes: the scatter reads each token row once and writes each routed row once
+// (HBM-bound copy); counts and scans touch 4 bytes per entry and per
+// (chunk, expert).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -30,6 +35,7 @@ namespace dgm {
 namespace {
 
 constexpr int kThreads = 256;
+using dev::i32x4;
 
 __device__ __forceinline__ int align_up(int x, int a) { return (x + a - 1) / a * a; }
 
@@ -46,51 +52,97 @@ __device__ __forceinline__ int topk_at(const MoeDispatchArgs& p, int t, int j) {
 
 __device__ __forceinline__ bool routed(const MoeDispatchArgs& p, int e) { return e >= 0 && e < p.num_experts; }
 
-// Workspace: counts [chunks][E] (exclusive prefixes after the scan), then
-// starts [E], totals [E], rows [1].
+// Workspace: counts [E][chunks] (exclusive prefixes over chunks after the
+// scan), then starts [E], totals [E], rows [1].
 __device__ __forceinline__ int32_t* ws_counts(const MoeDispatchArgs& p) { return p.ws; }
 __device__ __forceinline__ int32_t* ws_starts(const MoeDispatchArgs& p) {
     return p.ws + (int64_t)p.chunks * p.num_experts;
 }
 __device__ __forceinline__ int32_t* ws_totals(const MoeDispatchArgs& p) { return ws_starts(p) + p.num_experts; }
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+// One workgroup per chunk of kMoeChunkTokens tokens. Wave 0 walks the chunk's
+// entries in (token, slot) order, 64 at a time: each routed entry's rank among
+// the chunk's earlier entries of its expert (ballots over the lanes holding
+// that expert) goes to pos[t, j]; the per-expert counts go to counts[e][chunk].
 __global__ void __launch_bounds__(kThreads) moe_count_kernel(const MoeDispatchArgs p) {
-    __shared__ int cnt[kMoeMaxExperts];
-    for (int e = threadIdx.x; e < p.num_experts; e += kThreads) cnt[e] = 0;
-    __syncthreads();
-    const int t0 = blockIdx.x * kMoeChunkTokens;
+    __shared__ int run[kMoeMaxExperts];
+    __shared__ int ids[kMoeChunkTokens * kMoeMaxTopk];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = blockIdx.x;
+    const int t0 = c * kMoeChunkTokens;
     const int entries = min(kMoeChunkTokens, p.t - t0) * p.k;
-    for (int i = threadIdx.x; i < entries; i += kThreads) {
-        const int e = topk_at(p, t0 + i / p.k, i % p.k);
-        if (routed(p, e)) atomicAdd(&cnt[e], 1);
+    for (int e = threadIdx.x; e < p.num_experts; e += kThreads) run[e] = 0;
+    for (int i = threadIdx.x; i < entries; i += kThreads) ids[i] = topk_at(p, t0 + i / p.k, i % p.k);
+    __syncthreads();
+    if (wave == 0) {
+        for (int b = 0; b < entries; b += 64) {
+            const int i = b + lane;
+            const int e = i < entries ? ids[i] : -1;
+            const bool ok = i < entries && routed(p, e);
+            // peers: the routed lanes whose expert id equals this lane's, one
+            // ballot per id bit (ids < kMoeMaxExperts = 2^10)
+            static_assert(kMoeMaxExperts <= 1024, "expert ids fit 10 bits");
+            uint64_t peers = __ballot(ok);
+#pragma unroll
+            for (int bit = 0; bit < 10; ++bit) {
+                const bool set = (e >> bit) & 1;
+                const uint64_t m = __ballot(ok && set);
+                peers &= set ? m : ~m;
+            }
+            const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+            if (ok) {
+                const int base = run[e];
+                p.pos[(int64_t)t0 * p.k + i] = base + __popcll(peers & below);
+                if ((peers >> lane) == 1ull) run[e] = base + __popcll(peers);   // the group's last lane
+            }
+            // (all lanes read run[] before any lane of this batch writes it: one
+            // wave, in program order; the next batch's reads follow the writes)
+        }
     }
     __syncthreads();
     for (int e = threadIdx.x; e < p.num_experts; e += kThreads)
-        ws_counts(p)[(int64_t)blockIdx.x * p.num_experts + e] = cnt[e];
+        ws_counts(p)[(int64_t)e * p.chunks + c] = run[e];
 }
 
-__global__ void __launch_bounds__(1024) moe_scan_kernel(const MoeDispatchArgs p) {
-    int32_t* counts = ws_counts(p);
-    for (int e = threadIdx.x; e < p.num_experts; e += 1024) {
-        int run = 0;
-        for (int c = 0; c < p.chunks; ++c) {
-            const int v = counts[(int64_t)c * p.num_experts + e];
-            counts[(int64_t)c * p.num_experts + e] = run;
-            run += v;
+// One wave per expert: the exclusive prefix of its chunk counts (in place, 256
+// chunks per round, 4 consecutive chunks per lane), its total, and for the
+// masked layout masked_m = min(total, max_m).
+__global__ void __launch_bounds__(kThreads) moe_scan_kernel(const MoeDispatchArgs p) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    if (e >= p.num_experts) return;   // wave-uniform
+    int32_t* cnt = ws_counts(p) + (int64_t)e * p.chunks;
+    int carry = 0;
+    for (int c0 = 0; c0 < p.chunks; c0 += 256) {
+        const int c = c0 + lane * 4;
+        int v[4], s = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[q] = c + q < p.chunks ? cnt[c + q] : 0;
+            s += v[q];
         }
-        ws_totals(p)[e] = run;
+        const int incl = wave_inclusive_sum(s, lane);
+        int x = carry + incl - s;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (c + q < p.chunks) cnt[c + q] = x;
+            x += v[q];
+        }
+        carry += __shfl(incl, 63);
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int e = 0; e < p.num_experts; ++e) {
-            const int total = ws_totals(p)[e];
-            ws_starts(p)[e] = p.layout == kMoeMasked ? 0 : acc;
-            if (p.layout == kMoePsum) p.meta[e] = acc + total;                  // psum[e] = align(psum[e-1]) + count
-            if (p.layout == kMoeMasked) p.meta[e] = min(total, p.max_m);         // masked_m
-            if (p.layout != kMoeMasked) acc += align_up(total, p.alignment);
-        }
-        ws_totals(p)[p.num_experts] = acc;   // rows used by the segments
+    if (lane == 0) {
+        ws_totals(p)[e] = carry;
+        if (p.layout == kMoeMasked) p.meta[e] = min(carry, p.max_m);
     }
 }
 
@@ -102,9 +154,41 @@ __device__ __forceinline__ int64_t row_sf(const MoeDispatchArgs& p, int64_t r) {
     return p.layout == kMoeMasked ? (r / p.max_m) * p.sf_gs + (r % p.max_m) * p.sf_sm : r * p.sf_sm;
 }
 
-// Block e < E: expert e's padding rows; block E: m_indices = -1 past the segments.
-__global__ void __launch_bounds__(kThreads) moe_pad_kernel(const MoeDispatchArgs p) {
-    const int e = blockIdx.x;
+// Contiguous and psum layouts, one block: the exclusive prefix of the aligned
+// expert totals (E <= 4 * kThreads, 4 experts per thread) gives the segment
+// starts; also the psum ends and the rows the segments use.
+__global__ void __launch_bounds__(kThreads) moe_starts_kernel(const MoeDispatchArgs p) {
+    static_assert(kMoeMaxExperts <= 4 * kThreads, "4 experts per thread");
+    __shared__ int wsum[kThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int v[4], tot[4], s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = threadIdx.x * 4 + q;
+        tot[q] = e < p.num_experts ? ws_totals(p)[e] : 0;
+        v[q] = align_up(tot[q], p.alignment);
+        s += v[q];
+    }
+    const int incl = wave_inclusive_sum(s, lane);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int x = incl - s;
+    for (int w = 0; w < wave; ++w) x += wsum[w];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = threadIdx.x * 4 + q;
+        if (e < p.num_experts) {
+            ws_starts(p)[e] = x;
+            if (p.layout == kMoePsum) p.meta[e] = x + tot[q];   // psum[e] = align(psum[e-1]) + count
+        }
+        x += v[q];
+    }
+    if (threadIdx.x == kThreads - 1) ws_totals(p)[p.num_experts] = x;   // rows used by the segments
+}
+
+// Contiguous and psum layouts: e < E fills expert e's padding rows (zero A, SF
+// and weight, m_indices = -1); e = E sets m_indices = -1 past the segments.
+__device__ __forceinline__ void pad_block(const MoeDispatchArgs& p, int e) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (e == p.num_experts) {
         if (p.layout != kMoeContiguous) return;
@@ -112,11 +196,12 @@ __global__ void __launch_bounds__(kThreads) moe_pad_kernel(const MoeDispatchArgs
         for (int64_t r = used + threadIdx.x; r < p.cap_rows; r += kThreads) p.meta[r] = -1;
         return;
     }
-    const int total = ws_totals(p)[e];
-    const int r0 = ws_starts(p)[e] + total, r1 = ws_starts(p)[e] + align_up(total, p.alignment);
+    const int total = ws_totals(p)[e], start = ws_starts(p)[e];
+    const int r0 = start + total, r1 = start + align_up(total, p.alignment);
     for (int r = r0 + wave; r < r1; r += kThreads / 64) {
         uint8_t* a = p.a + row_a(p, r);
-        for (int c = lane * 16; c < p.kdim; c += 64 * 16) *reinterpret_cast<uint4*>(a + c) = uint4{0, 0, 0, 0};
+        for (int c = lane * 16; c < p.kdim; c += 64 * 16)
+            __builtin_nontemporal_store(i32x4{0, 0, 0, 0}, reinterpret_cast<i32x4*>(a + c));
         for (int c = lane; c < p.sfk; c += 64) p.sf[row_sf(p, r) + (int64_t)c * p.sf_sk_o] = 0.f;
         if (lane == 0) {
             if (p.w_out) p.w_out[r] = 0.f;
@@ -125,62 +210,74 @@ __global__ void __launch_bounds__(kThreads) moe_pad_kernel(const MoeDispatchArgs
     }
 }
 
-__global__ void __launch_bounds__(kThreads) moe_scatter_kernel(const MoeDispatchArgs p) {
-    __shared__ int run[kMoeMaxExperts];
-    __shared__ int lpos[kMoeChunkTokens * kMoeMaxTopk];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = blockIdx.x;
-    const int t0 = c * kMoeChunkTokens;
-    const int entries = min(kMoeChunkTokens, p.t - t0) * p.k;
-    for (int e = threadIdx.x; e < p.num_experts; e += kThreads)
-        run[e] = ws_starts(p)[e] + ws_counts(p)[(int64_t)c * p.num_experts + e];
-    __syncthreads();
-    if (wave == 0) {
-        // entries in order, 64 at a time: rank among earlier lanes of the same
-        // expert, then the last lane of each expert advances its counter
-        for (int b = 0; b < entries; b += 64) {
-            const int i = b + lane;
-            const int e = i < entries ? topk_at(p, t0 + i / p.k, i % p.k) : -1;
-            const bool ok = i < entries && routed(p, e);
-            uint64_t left = __ballot(ok), peers = 0;
-            while (left) {
-                const int leader = __builtin_ctzll(left);
-                const int v = __shfl(e, leader);
-                const uint64_t m = __ballot(ok && e == v);
-                if (ok && e == v) peers = m;
-                left &= ~m;
+// One wave per token: lane j < k turns slot j's chunk rank into its output row
+// (segment start + the expert's prefix over earlier chunks + the rank; for the
+// masked layout -1 past max_m) and writes pos, the row weight and m_indices;
+// then the wave reads the token's K bytes once, 8 KB per round (8 x 16 B per
+// lane in flight), and stores them to each routed row, then the SF row. The
+// first pad_blocks blocks (E + 1 for the contiguous and psum layouts, else 0)
+// run pad_block instead, beside the copies.
+__global__ void __launch_bounds__(kThreads) moe_scatter_kernel(const MoeDispatchArgs p, int pad_blocks) {
+    if ((int)blockIdx.x < pad_blocks) {
+        pad_block(p, blockIdx.x);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const int t = (blockIdx.x - pad_blocks) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (t >= p.t) return;   // wave-uniform
+    // The row's first 8 KB are loaded before the rows are looked up (the two
+    // are independent), so the lookup's load latency hides behind them.
+    const i32x4* src = reinterpret_cast<const i32x4*>(p.x + (int64_t)t * p.ldx);
+    const int units = p.kdim / 16;
+    i32x4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int u = q * 64 + lane;
+        if (u < units) v[q] = src[u];
+    }
+    int flat = -1;
+    if (lane < p.k) {
+        const int e = topk_at(p, t, lane);
+        if (routed(p, e)) {
+            const int64_t pi = (int64_t)t * p.k + lane;
+            const int r = (p.layout == kMoeMasked ? 0 : ws_starts(p)[e]) +
+                          ws_counts(p)[(int64_t)e * p.chunks + t / kMoeChunkTokens] + p.pos[pi];
+            flat = p.layout == kMoeMasked ? (r < p.max_m ? e * p.max_m + r : -1) : r;
+            if (flat >= 0) {
+                if (p.w_out) p.w_out[flat] = p.topk_w ? p.topk_w[(int64_t)t * p.w_st + (int64_t)lane * p.w_sk] : 1.f;
+                if (p.layout == kMoeContiguous) p.meta[flat] = e;
             }
-            const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-            int r = -1;
-            if (ok) {
-                const int base = run[e];
-                r = base + __popcll(peers & below);
-                if ((peers >> lane) == 1ull) run[e] = base + __popcll(peers);   // the group's last lane
+        }
+        p.pos[(int64_t)t * p.k + lane] = flat;
+    }
+    // The rows are written once and read by the next kernel, not by this one:
+    // non-temporal stores (about 1.5x the copy rate of plain ones here).
+    for (int u0 = 0; u0 < units; u0 += 64 * 8) {
+        if (u0 > 0) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int u = u0 + q * 64 + lane;
+                if (u < units) v[q] = src[u];
             }
-            int flat = -1;
-            if (ok) flat = p.layout == kMoeMasked ? (r < p.max_m ? e * p.max_m + r : -1) : r;
-            if (i < entries) {
-                lpos[i] = flat;
-                p.pos[(int64_t)(t0 + i / p.k) * p.k + i % p.k] = flat;
+        }
+        for (int j = 0; j < p.k; ++j) {
+            const int r = __builtin_amdgcn_readfirstlane(__shfl(flat, j));
+            if (r < 0) continue;   // wave-uniform
+            i32x4* dst = reinterpret_cast<i32x4*>(p.a + row_a(p, r));
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int u = u0 + q * 64 + lane;
+                if (u < units) __builtin_nontemporal_store(v[q], dst + u);
             }
-            // (all lanes read run[] before any lane of this batch writes it: one
-            // wave, in program order; the next batch's reads follow the writes)
         }
     }
-    __syncthreads();
-    for (int i = wave; i < entries; i += kThreads / 64) {
-        const int r = lpos[i];
-        if (r < 0) continue;   // wave-uniform
-        const int t = t0 + i / p.k, j = i % p.k;
-        const uint8_t* src = p.x + (int64_t)t * p.ldx;
-        uint8_t* dst = p.a + row_a(p, r);
-        for (int col = lane * 16; col < p.kdim; col += 64 * 16)
-            *reinterpret_cast<uint4*>(dst + col) = *reinterpret_cast<const uint4*>(src + col);
-        for (int s = lane; s < p.sfk; s += 64)
-            p.sf[row_sf(p, r) + (int64_t)s * p.sf_sk_o] = p.x_sf[(int64_t)t * p.sf_st + (int64_t)s * p.sf_sk];
-        if (lane == 0) {
-            if (p.w_out) p.w_out[r] = p.topk_w ? p.topk_w[(int64_t)t * p.w_st + (int64_t)j * p.w_sk] : 1.f;
-            if (p.layout == kMoeContiguous) p.meta[r] = topk_at(p, t, j);
+    for (int s0 = 0; s0 < p.sfk; s0 += 64) {
+        const int s = s0 + lane;
+        const float sv = s < p.sfk ? p.x_sf[(int64_t)t * p.sf_st + (int64_t)s * p.sf_sk] : 0.f;
+        for (int j = 0; j < p.k; ++j) {
+            const int r = __builtin_amdgcn_readfirstlane(__shfl(flat, j));
+            if (r < 0) continue;
+            if (s < p.sfk) p.sf[row_sf(p, r) + (int64_t)s * p.sf_sk_o] = sv;
         }
     }
 }
@@ -309,14 +406,17 @@ void launch_moe_dispatch(const MoeDispatchArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(moe_count_kernel, dim3(a.chunks), dim3(kThreads), 0, stream, a);
         DG_HIP_CHECK(hipGetLastError());
     }
-    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, stream, a);
+    hipLaunchKernelGGL(moe_scan_kernel, dim3((a.num_experts + kThreads / 64 - 1) / (kThreads / 64)), dim3(kThreads), 0,
+                       stream, a);
     DG_HIP_CHECK(hipGetLastError());
+    const int pad_blocks = a.layout == kMoeMasked ? 0 : a.num_experts + 1;
     if (a.layout != kMoeMasked) {
-        hipLaunchKernelGGL(moe_pad_kernel, dim3(a.num_experts + 1), dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL(moe_starts_kernel, dim3(1), dim3(kThreads), 0, stream, a);
         DG_HIP_CHECK(hipGetLastError());
     }
-    if (a.t > 0) {
-        hipLaunchKernelGGL(moe_scatter_kernel, dim3(a.chunks), dim3(kThreads), 0, stream, a);
+    const int64_t blocks = pad_blocks + ((int64_t)a.t + kThreads / 64 - 1) / (kThreads / 64);
+    if (blocks > 0) {
+        hipLaunchKernelGGL(moe_scatter_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a, pad_blocks);
         DG_HIP_CHECK(hipGetLastError());
     }
 }
