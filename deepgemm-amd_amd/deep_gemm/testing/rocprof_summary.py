@@ -31,8 +31,9 @@ import os
 import sys
 
 GEMM_KEYS = ('fp8_gemm_1d2d', 'fp8_fp4_gemm', 'fp8_gemm_1d2d_pipe', 'fp8_gemm_masked_stream', 'fp8_gemm_1d1d',
-             'fp8_gemm_tinym')
+             'fp8_gemm_tinym', 'fp8_gemm_splitk', 'moe_swiglu_cast_kernel')
 CAST_KEYS = ('per_token_cast_kernel',)   # the cast workload's kernel (GEMM workloads also cast while setting up)
+MOE_DISPATCH_KEYS = ('moe_count_kernel', 'moe_scan_kernel', 'moe_starts_kernel', 'moe_scatter_kernel')
 COPY_KEY = 'neg_kernel'
 _KEYS = GEMM_KEYS
 
@@ -91,10 +92,13 @@ def mfma_utilization(busy_cycles: float, gui_cycles: float, kernel_us: float, si
 
 def dispatches_per_call(config: str) -> int:
     """Kernels one bench launch dispatches: a dense column split, a contiguous row
-    split or the split-K kernel (partials, then the reduction) runs two; a launch
-    of several library calls (configs joined by ' + ') sums them."""
+    split or the split-K kernel (partials, then the reduction) runs two; a MoE
+    dispatch runs its count, scan, (segment starts,) scatter kernels; a launch of
+    several library calls (configs joined by ' + ') sums them."""
     if ' + ' in config:
         return sum(dispatches_per_call(c) for c in config.split(' + '))
+    if config.startswith('moe_dispatch'):   # count, scan, (starts,) scatter
+        return 3 if 'layout=masked' in config else 4
     return 2 if ('split_n=' in config or 'split_m=' in config or ' splits=' in config) else 1
 
 
@@ -137,7 +141,13 @@ def summarize(args):
     global _KEYS
     bench = json.loads(open(args.bench_json).read().strip().splitlines()[-1])
     roof = bench['roofline']
-    _KEYS = CAST_KEYS if roof.get('kernel') == ['per_token_cast'] else GEMM_KEYS
+    kernels = roof.get('kernel') or []
+    if kernels == ['per_token_cast']:
+        _KEYS = CAST_KEYS
+    elif kernels and all(k.startswith('moe_dispatch') for k in kernels):
+        _KEYS = MOE_DISPATCH_KEYS
+    else:
+        _KEYS = GEMM_KEYS
     names = list(roof['per_launch_us'].keys())
     warmup = args.warmup if args.warmup is not None else bench['warmup']
     steps = args.steps if args.steps is not None else bench['steps']

@@ -91,6 +91,13 @@ def test_dispatches_per_call_split_k_and_joined_calls():
                                   'moe_swiglu_cast gran_k=128 m=33408 n=2048') == 2
 
 
+def test_dispatches_per_call_moe_dispatch():
+    """count, scan, segment starts and scatter; the masked layout has no starts."""
+    assert rs.dispatches_per_call('moe_dispatch layout=contiguous experts=256 t=4096 k=8 kdim=7168') == 4
+    assert rs.dispatches_per_call('moe_dispatch layout=psum experts=256 t=4096 k=8 kdim=7168') == 4
+    assert rs.dispatches_per_call('moe_dispatch layout=masked experts=16 t=512 k=8 kdim=7168') == 3
+
+
 def test_mfma_clock_capped_at_chip_maximum():
     """GRBM_GUI_ACTIVE over the traced duration gives the clock; above 2.4 GHz the
     counter included time outside the kernel, so the busy fraction is taken over
