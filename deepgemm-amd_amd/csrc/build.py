@@ -29,7 +29,7 @@ COMMON = ['-O3', '-std=c++20', '-fPIC', '-Wall', '-I', INCLUDE, '-I', HERE]
 # MFMA results are kept in architectural VGPRs (the promotion FMAs read them
 # directly; AGPR destinations would cost a v_accvgpr_read per element).
 HIP_FLAGS = ['--offload-arch=' + ARCH, '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
-             '-ffp-contract=fast', '-mllvm', '-amdgpu-mfma-vgpr-form=true',
+             '-ffp-contract=fast-honor-pragmas', '-mllvm', '-amdgpu-mfma-vgpr-form=true',
              # the LDS-DMA asm helpers clobber M0, which no compiled code here keeps live
              '-Wno-inline-asm']
 CXX_FLAGS = ['-D__HIP_PLATFORM_AMD__', '-I', os.path.join(ROCM, 'include')]

@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(kThreads) moe_combine_kernel(const CombineArgs
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float yv = bf16_to_f32(e & 1 ? vw[e >> 1] >> 16 : vw[e >> 1] & 0xFFFFu);
-            acc[e] = __fadd_rn(acc[e], p.topk_w ? __fmul_rn(w, yv) : yv);
+            acc[e] = dev::f32_add(acc[e], p.topk_w ? dev::f32_mul(w, yv) : yv);
         }
     }
     uint32_t o[4];

@@ -8,7 +8,9 @@
 //   gate, up   the BF16 values of the L1 GEMM's output (the fused epilogue rounds
 //              its FP32 accumulators to BF16 first, as the BF16 D would hold them)
 //   clamp > 0  up = min(c, max(-c, up)), gate = min(c, gate)
-//   y          silu(gate) * up * w, each step rounded to FP32 (no contraction)
+//   y          silu(gate) * up * w, each step rounded to FP32 (no contraction),
+//              silu from exp_f32_steps (IEEE single steps only, so the
+//              oracle reproduces every bit)
 //   amax       max |y| over the 1 x GRAN group, clamped at 1e-4
 //   sf         amax * fl32(1/448);  code = e4m3(y * (1 / sf))
 //
@@ -28,14 +30,64 @@
 namespace dgm {
 namespace dev {
 
+// Single-precision multiply / add / subtract, rounded to nearest and never fused
+// into an FMA with a neighbouring operation (the build contracts with
+// -ffp-contract=fast-honor-pragmas; these bodies turn it off). __fmul_rn and
+// friends are plain operators in this toolchain's headers and may be fused.
+__device__ __forceinline__ float f32_mul(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float f32_add(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float f32_sub(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+
+// exp(x) for x in [-87, 88] from single-precision multiplies and adds, each
+// rounded to nearest (no contraction), so that the same steps in float32 numpy
+// give the same bits (the oracle restates them): Cody-Waite reduction
+// x = n ln2 + r with n = rint(x log2 e), ln2 split into a 9-bit high part (n *
+// hi is exact) and a low part; exp(r) by the degree-7 Taylor polynomial in
+// Horner form (|r| <= 0.35: truncation below 5e-9); times 2^n through the
+// exponent field. Measured against float64 exp: at most 1.2 ulp.
+__device__ __forceinline__ float exp_f32_steps(float x) {
+    const float n = rintf(f32_mul(x, __uint_as_float(0x3fb8aa3bu)));                  // log2(e)
+    const float r = f32_sub(f32_sub(x, f32_mul(n, __uint_as_float(0x3f318000u))),   // ln2 high
+                              f32_mul(n, __uint_as_float(0xb95e8083u)));                 // ln2 low
+    float p = __uint_as_float(0x39500d01u);                                                // 1/5040
+    p = f32_add(f32_mul(p, r), __uint_as_float(0x3ab60b61u));                          // 1/720
+    p = f32_add(f32_mul(p, r), __uint_as_float(0x3c088889u));                          // 1/120
+    p = f32_add(f32_mul(p, r), __uint_as_float(0x3d2aaaabu));                          // 1/24
+    p = f32_add(f32_mul(p, r), __uint_as_float(0x3e2aaaabu));                          // 1/6
+    p = f32_add(f32_mul(p, r), 0.5f);
+    p = f32_add(f32_mul(p, r), 1.0f);
+    p = f32_add(f32_mul(p, r), 1.0f);
+    return f32_mul(p, __int_as_float(((int)n + 127) << 23));
+}
+
+// silu(g) = g / (1 + exp(-g)): 1 + exp(-g) is 1 for g > 87 (exp(-g) < 2^-125),
+// +inf for g < -88, NaN for NaN; then one correctly rounded division.
+__device__ __forceinline__ float silu_f32(float g) {
+    const float x = -g;
+    float den;
+    if (x != x) den = x;
+    else if (x > 88.0f) den = __builtin_inff();
+    else if (x < -87.0f) den = 1.0f;
+    else den = f32_add(1.0f, exp_f32_steps(x));
+    return __fdiv_rn(g, den);
+}
+
 // y = silu(gate) * up * w (after the optional clamp).
 __device__ __forceinline__ float swiglu_weighted(float g, float u, float w, float clamp) {
     if (clamp > 0.f) {
         u = fminf(clamp, fmaxf(-clamp, u));
         g = fminf(clamp, g);
     }
-    const float s = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
-    return __fmul_rn(__fmul_rn(s, u), w);
+    return f32_mul(f32_mul(silu_f32(g), u), w);
 }
 
 // OCP e4m3 code of v by explicit rounding (saturating to 0x7F | sign past 464,
@@ -66,11 +118,11 @@ __device__ __forceinline__ uint2 quantize_group8(const float (&y)[8], float& sf_
 #pragma unroll
     for (int o = TPG / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
     amax = fmaxf(amax, 1e-4f);
-    const float sf = __fmul_rn(amax, 1.0f / 448.0f);
+    const float sf = f32_mul(amax, 1.0f / 448.0f);
     const float inv = __fdiv_rn(1.0f, sf);
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __fmul_rn(y[e], inv);
+    for (int e = 0; e < 8; ++e) v[e] = f32_mul(y[e], inv);
     uint32_t lo = 0, hi = 0;
     if (__builtin_expect(__ballot(!(amax < __uint_as_float(0x7F800000u))) == 0, 1)) {
         int l = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
@@ -161,7 +213,7 @@ struct SwigluTile {
 // tile that computes nothing (ensure_zero_padding).
 template <int NT>
 __device__ __forceinline__ void swiglu_zero_rows(const SwigluOut& o, int g, int ib, int r_lo, int r_hi, int tid) {
-    const float sf = __fmul_rn(1e-4f, 1.0f / 448.0f);   // amax of an all-zero group, clamped
+    const float sf = f32_mul(1e-4f, 1.0f / 448.0f);   // amax of an all-zero group, clamped
     for (int idx = tid; idx < (r_hi - r_lo) * 16; idx += NT) {
         const int m = r_lo + idx / 16, c16 = idx % 16;
         *reinterpret_cast<uint2*>(o.q + (int64_t)g * o.q_gs + (int64_t)m * o.ldq + ib * 128 + 8 * c16) = uint2{0u, 0u};

@@ -42,12 +42,6 @@ def _alloc_out(rows_shape, inter):
     return q, sf
 
 
-def _unfused_contiguous(a, w, d_rows, gl, inter, rw, psum, zero_padding):
-    h = torch.zeros((d_rows, 2 * inter), dtype=torch.bfloat16, device=DEV)
-    deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, w, h, gl, use_psum_layout=psum, ensure_zero_padding=zero_padding)
-    return deep_gemm.moe_swiglu_apply_weight_to_fp8(h, rw, None if psum else gl, None)
-
-
 def _psum_layout(ms, align):
     ends, starts, acc = [], [], 0
     for mi in ms:

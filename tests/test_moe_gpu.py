@@ -13,7 +13,6 @@ import pytest
 import torch
 
 import deep_gemm
-from oracle import fp8 as ofp8
 from oracle import gemm as ogemm
 from oracle import moe as omoe
 from oracle import quant as oquant
@@ -112,17 +111,24 @@ def test_swiglu_cast_vs_oracle(gran, clamp):
     # rows marked padding are written as +0 codes (a product with 0 would give -0 for negative x)
     rq, rsf = omoe.swiglu_apply_weight_to_fp8(np.where((layout >= 0)[:, None], x, 0.0), w, clamp, gran)
     gq, gsf = q.view(torch.uint8).cpu().numpy(), sf.cpu().numpy()
-    ulps = np.abs(gsf.view(np.int32).astype(np.int64) - rsf.view(np.int32).astype(np.int64))
-    same = gq == rq
-    print(f'swiglu gran={gran} clamp={clamp}: scales equal {np.mean(ulps == 0):.4f}, max {ulps.max()} ulp; '
-          f'codes equal {same.mean():.5f}', flush=True)
-    assert ulps.max() <= 4
-    assert same.mean() >= 0.999
-    gv, rv = ofp8.e4m3_decode(gq[~same]), ofp8.e4m3_decode(rq[~same])
-    assert np.all(np.sign(gv) * np.sign(rv) >= 0)
-    assert np.all(np.abs((gq[~same] & 0x7F).astype(int) - (rq[~same] & 0x7F).astype(int)) <= 1)
+    print(f'swiglu gran={gran} clamp={clamp}: codes equal {np.mean(gq == rq):.6f}, '
+          f'scales equal {np.mean(gsf.view(np.int32) == rsf.view(np.int32)):.6f}', flush=True)
+    # bit-exact: the kernel runs the oracle's float32 steps, exp included
+    assert np.array_equal(gq, rq)
+    assert np.array_equal(gsf.view(np.int32), rsf.view(np.int32))
     pad = layout < 0
     assert np.all(gq[pad] == 0)
+
+
+def test_combine_slot_order():
+    """The float32 sums run in slot order: rows 2^24, -2^24 and 1 give 1 for
+    slots (0, 1, 2) and 0 for (0, 2, 1), as the oracle's do."""
+    y = np.repeat(np.array([[2.0 ** 24], [-2.0 ** 24], [1.0]], np.float32), 8, axis=1)
+    pos = np.array([[0, 1, 2], [0, 2, 1]], np.int32)
+    out = deep_gemm.moe_combine(torch.from_numpy(y).bfloat16().to(DEV), gen.to_dev(pos), None)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.array_equal(got, omoe.combine(y, pos)) and np.all(got[0] == 1.0) and np.all(got[1] == 0.0)
 
 
 @pytest.mark.parametrize('weighted', [False, True])

@@ -405,15 +405,55 @@ def test_moe_dispatch_copies_rows_and_zero_padding():
     assert np.all(out['a'][pad] == 0) and np.all(out['sf'][pad] == 0) and np.all(out['weights'][pad] == 0)
 
 
+def test_exp_f32_within_1_5_ulp_of_float64():
+    """The float32 exp restatement (the device kernels run the same steps): within
+    1.5 ulp of float64 exp over 4 million uniform arguments in [-87, 88], 2 million
+    in [-1, 1] and every 7th float32 of [0.5, 1); exact at 0; finite at both ends
+    of its domain."""
+    from oracle import moe as omoe
+    rng = np.random.default_rng(61)
+    xs = np.concatenate([rng.uniform(-87, 88, 4_000_000).astype(np.float32),
+                         np.linspace(-1, 1, 2_000_001, dtype=np.float32),
+                         (np.arange(0, 2 ** 23, 7, dtype=np.uint32) | np.uint32(0x3f000000)).view(np.float32)])
+    got = omoe.exp_f32(xs).astype(np.float64)
+    ref = np.exp(xs.astype(np.float64))
+    ulps = np.abs(got - ref) / np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert ulps.max() <= 1.5, ulps.max()
+    assert omoe.exp_f32(np.float32(0.0)) == np.float32(1.0)
+    ends = omoe.exp_f32(np.array([-87.0, 88.0], np.float32))
+    assert np.all(np.isfinite(ends)) and np.all(ends > 0)
+
+
+def test_silu_f32_special_values():
+    """silu(0) = 0; silu(g) = g for g > 87 (1 + exp(-g) rounds to 1); -0 for
+    g < -88 (exp(-g) overflows); NaN in, NaN out; and within 2 ulp (relative
+    2.4e-7) of the float64 closed form on a million normal samples."""
+    from scipy.special import expit
+    from oracle import moe as omoe
+    g = np.array([0.0, 87.5, 100.0, -88.5, -1e4, np.nan], np.float32)
+    s = omoe.silu_f32(g)
+    assert s[0] == 0.0 and s[1] == np.float32(87.5) and s[2] == np.float32(100.0)
+    assert s[3] == 0.0 and np.signbit(s[3]) and s[4] == 0.0 and np.isnan(s[5])
+    x = (np.random.default_rng(62).standard_normal(1_000_000) * 8).astype(np.float32)
+    ref = x.astype(np.float64) * expit(x.astype(np.float64))
+    rel = np.abs(omoe.silu_f32(x).astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() < 2.4e-7, rel.max()
+
+
 def test_moe_swiglu_closed_forms():
     from scipy.special import expit
     from oracle import moe as omoe
     rng = np.random.default_rng(6)
     x = gen_bf16((7, 64), rng)
-    w = rng.random(7)
+    w = rng.random(7).astype(np.float32)
     y = omoe.swiglu_apply_weight(x, w)
+    assert y.dtype == np.float32
     g, u = x[:, :32].astype(np.float64), x[:, 32:].astype(np.float64)
-    assert np.allclose(y, g * expit(g) * u * w[:, None], rtol=1e-14, atol=0)
+    # three float32 roundings after silu's (division, * up, * w): within 4 ulp
+    assert np.allclose(y, g * expit(g) * u * w[:, None].astype(np.float64), rtol=5e-7, atol=0)
+    # the steps themselves: silu, then * up, then * w, each rounded to float32
+    step = ((omoe.silu_f32(x[:, :32]) * x[:, 32:]).astype(np.float32) * w[:, None]).astype(np.float32)
+    assert np.array_equal(y, step)
     z = omoe.swiglu_apply_weight(np.concatenate([np.zeros((1, 4)), np.full((1, 4), 3.0)], axis=1))
     assert np.all(z == 0.0)                      # silu(0) = 0
     c = omoe.swiglu_apply_weight(np.array([[50.0, -50.0, 2.0, 2.0]]), clamp=7.0)
@@ -421,6 +461,30 @@ def test_moe_swiglu_closed_forms():
     q, sf = omoe.swiglu_apply_weight_to_fp8(x, w, gran_k=32)
     qq, ss = oquant.per_token_cast_to_fp8(omoe.swiglu_apply_weight(x, w).astype(np.float32), False, 32)
     assert np.array_equal(q, qq) and np.array_equal(sf, ss)
+
+
+def test_moe_combine_exact_sums_and_slot_order():
+    """Where every product and partial sum is exactly representable (bf16 values
+    times power-of-two weights, small magnitudes) combine equals the exact sum;
+    and the float32 accumulation runs in slot order: with rows 2^24, -2^24 and 1,
+    slots (0, 1, 2) give (2^24 - 2^24) + 1 = 1, slots (0, 2, 1) give
+    (2^24 + 1) - 2^24 = 0 (2^24 + 1 rounds to 2^24 in float32)."""
+    from oracle import moe as omoe
+    rng = np.random.default_rng(63)
+    t_n, k, rows, n = 6, 4, 20, 16
+    y = (rng.integers(-64, 64, size=(rows, n)) / 8.0).astype(np.float32)      # exact in bf16
+    pos = rng.integers(-1, rows, size=(t_n, k))
+    w = (2.0 ** rng.integers(-3, 3, size=(t_n, k))).astype(np.float32)
+    exact = np.zeros((t_n, n))
+    for t in range(t_n):
+        for j in range(k):
+            if pos[t, j] >= 0:
+                exact[t] += w[t, j] * y[pos[t, j]].astype(np.float64)
+    out = omoe.combine(y, pos, w)
+    assert np.array_equal(out, oquant.bf16_round(exact.astype(np.float32)))
+    yy = np.array([[2.0 ** 24], [-2.0 ** 24], [1.0]], np.float32)
+    assert omoe.combine(yy, np.array([[0, 1, 2]]))[0, 0] == 1.0
+    assert omoe.combine(yy, np.array([[0, 2, 1]]))[0, 0] == 0.0
 
 
 def test_moe_combine_against_vectorized_sum():
