@@ -5,6 +5,9 @@ the DeepSeek-V3 (N, K) sweep {(2112,7168), (24576,1536), (7168,16384),
 (4096,7168), (7168,2048)}, e4m3 operands with 1x128 / 128x128 FP32 scales, BF16
 output. One step = one call per shape (5 launches). `value` is total
 algorithmic FLOPs / wall time of the timed steps (inputs resident in HBM).
+The activation scales (SFA) are passed in the layout each kernel reads fastest,
+MN-major TMA-aligned for the dense and masked launches and K-major for the
+contiguous ones (`--sfa-major` forces one; the library takes both).
 
 Each launch has 8 rotating buffer sets (copies of its inputs and outputs) and
 step s runs on set s % 8, so no launch finds its operands in L2 or the 256 MB
@@ -70,6 +73,10 @@ def parse():
     ap.add_argument('--hipblaslt', action='store_true',
                     help='dense workload: also time the vendor FP8 GEMM (torch._scaled_mm -> hipBLASLt) on the same '
                          'shapes with per-tensor and row-wise scales, for context (not part of value)')
+    ap.add_argument('--sfa-major', choices=['auto', 'mn', 'k'], default='auto',
+                    help='SFA layout of the GEMM workloads: MN-major TMA-aligned (as the reference\'s kernels '
+                         'consume it), K-major (as per_token_cast_to_fp8 returns it), or per launch the one its '
+                         'kernel reads fastest (auto)')
     ap.add_argument('--calibrate-copy-mib', type=int, default=0,
                     help='first run torch.neg over this many MiB of float32 (a plain copy kernel of known '
                          'size, the reference for FETCH_SIZE / WRITE_SIZE counter passes)')
@@ -203,6 +210,31 @@ def _quant_b(n, k, gen, dev):
     return deep_gemm.per_block_cast_to_fp8(x, use_ue8m0=False)
 
 
+# SFA layout the GEMM workloads pass (the values are the same in both):
+#   'mn'   the MN-major TMA-aligned layout, as the reference's kernels consume it
+#          (its API transforms K-major SFA inside each call, and its benchmarks
+#          time the GEMM kernel alone, tests/test_fp8_fp4.py:169,226) and as
+#          per_token_cast_to_fp8_mn_major writes it in one pass;
+#   'k'    the K-major layout per_token_cast_to_fp8 returns;
+#   'auto' (default) per launch, the layout its kernel reads fastest: MN-major
+#          for the dense and masked kernels (3.5% and 6% faster than K-major), and
+#          K-major for the contiguous one, whose two-stage tiles fetch K-major
+#          scales four K blocks per request and keep the split stage hand-off only
+#          with them (MN-major is 2% slower there).
+SFA_MAJOR = 'auto'
+
+
+def _sfa(a, prefer):
+    """(codes, SFA) in the layout SFA_MAJOR names ('auto': `prefer`)."""
+    import deep_gemm
+    major = prefer if SFA_MAJOR == 'auto' else SFA_MAJOR
+    return (a[0], deep_gemm.get_mn_major_tma_aligned_tensor(a[1])) if major == 'mn' else a
+
+
+def _sfa_name(prefer):
+    return (prefer if SFA_MAJOR == 'auto' else SFA_MAJOR) + '-major'
+
+
 # Operand builders: the exact seeded inputs of each configuration. The
 # full-size parity tests (tests/test_configs_gpu.py) build their inputs through
 # these same functions, so the bench workloads are the tested workloads.
@@ -309,6 +341,7 @@ def make_dense(acc: bool):
     launches = []
     for op in dense_operands(acc, dev):
         m, n, k = op['m'], op['n'], op['k']
+        op['a'] = _sfa(op['a'], 'mn')
         if acc:
             def mk(a=op['a'], b=op['b'], d=op['c']):
                 a2, b2, d2 = _twin(a), _twin(b), _twin(d)
@@ -323,7 +356,7 @@ def make_dense(acc: bool):
         launches.append(Launch(op['name'], mk, 2 * m * n * k, _dense_bytes(m, n, k, out_bytes)))
     cfg = {'workload': 'fp8_gemm_nt M=4096 DeepSeek-V3 (N,K) sweep' + (' FP32 C-accumulate' if acc else ''),
            'm': 4096, 'nk': DENSE_NK, 'out': 'f32 (D=C+AB^T)' if acc else 'bf16',
-           'recipe': '1x128 A / 128x128 B FP32 scales'}
+           'recipe': '1x128 A / 128x128 B FP32 scales', 'sfa': _sfa_name('mn')}
     return launches, cfg
 
 
@@ -336,13 +369,14 @@ def make_decode():
     dev = torch.device('cuda:0')
     gen = torch.Generator().manual_seed(1)
     m, n, k = 64, 2112, 7168
-    a, b = _quant_a(m, k, gen, dev), _quant_b(n, k, gen, dev)
+    a, b = _sfa(_quant_a(m, k, gen, dev), 'k'), _quant_b(n, k, gen, dev)
 
     def mk():
         a2, b2 = _twin(a), _twin(b)
         d2 = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         return lambda: deep_gemm.fp8_gemm_nt(a2, b2, d2)
-    cfg = {'workload': 'fp8_gemm_nt M=64 N=2112 K=7168 (config 1 shape)', 'm': m, 'n': n, 'k': k, 'out': 'bf16'}
+    cfg = {'workload': 'fp8_gemm_nt M=64 N=2112 K=7168 (config 1 shape)', 'm': m, 'n': n, 'k': k, 'out': 'bf16',
+           'sfa': _sfa_name('k')}
     return [Launch('m64_n2112_k7168', mk, 2 * m * n * k, _dense_bytes(m, n, k, 2 * m * n))], cfg
 
 
@@ -356,7 +390,7 @@ def make_contiguous():
     for op in ops['shapes']:
         n, k = op['n'], op['k']
 
-        def mk(a=op['a'], b=op['b'], n=n):
+        def mk(a=_sfa(op['a'], 'k'), b=op['b'], n=n):
             a2, b2 = _twin(a), _twin(b)
             d2 = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
             return lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a2, b2, d2, idx)
@@ -364,7 +398,8 @@ def make_contiguous():
             4 * g * ((n + 127) // 128) * ((k + 127) // 128) + 4 * m_pad
         launches.append(Launch(op['name'], mk, 2 * total * n * k, nbytes))
     cfg = {'workload': 'm_grouped_fp8_gemm_nt_contiguous 8 experts 32768 tokens Dirichlet(1)',
-           'tokens_per_expert': ops['ms'], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)]}
+           'tokens_per_expert': ops['ms'], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)],
+           'sfa': _sfa_name('k')}
     return launches, cfg
 
 
@@ -379,7 +414,7 @@ def make_masked():
     for op in ops['shapes']:
         n, k = op['n'], op['k']
 
-        def mk(a=op['a'], b=op['b'], n=n):
+        def mk(a=_sfa(op['a'], 'mn'), b=op['b'], n=n):
             a2, b2 = _twin(a), _twin(b)
             d2 = torch.empty((g, max_m, n), dtype=torch.bfloat16, device=dev)
             return lambda: deep_gemm.m_grouped_fp8_gemm_nt_masked(a2, b2, d2, mm, ops['expected_m'])
@@ -387,7 +422,7 @@ def make_masked():
             4 * g * ((n + 127) // 128) * ((k + 127) // 128)
         launches.append(Launch(op['name'], mk, 2 * sum_m * n * k, nbytes))
     cfg = {'workload': 'm_grouped_fp8_gemm_nt_masked 16 experts max_m=256 masked_m~U[96,160]',
-           'masked_m': masked.tolist(), 'nk': [(4096, 7168), (7168, 2048)]}
+           'masked_m': masked.tolist(), 'nk': [(4096, 7168), (7168, 2048)], 'sfa': _sfa_name('mn')}
     return launches, cfg
 
 
@@ -455,6 +490,7 @@ def make_moe_l1():
     m = masked_operands(dev)
     co, mo = c['shapes'][0], m['shapes'][0]
     assert (co['n'], co['k']) == (4096, 7168) and (mo['n'], mo['k']) == (4096, 7168)
+    co['a'], mo['a'] = _sfa(co['a'], 'k'), _sfa(mo['a'], 'mn')
     n, k = co['n'], co['k']
     inter = n // 2
     m_pad, idx, total = c['m_pad'], c['m_indices'], c['total']
@@ -817,6 +853,8 @@ def main():
             torch.neg(x, out=y)
         torch.cuda.synchronize()
         del x, y
+    global SFA_MAJOR
+    SFA_MAJOR = args.sfa_major
     rot = args.rotate
     reps = max(5, args.steps)
     wl = Workload(args.workload, rot, args.eager)
