@@ -5,9 +5,9 @@ the DeepSeek-V3 (N, K) sweep {(2112,7168), (24576,1536), (7168,16384),
 (4096,7168), (7168,2048)}, e4m3 operands with 1x128 / 128x128 FP32 scales, BF16
 output. One step = one call per shape (5 launches). `value` is total
 algorithmic FLOPs / wall time of the timed steps (inputs resident in HBM).
-The activation scales (SFA) are passed in the layout each kernel reads fastest,
-MN-major TMA-aligned for the dense and masked launches and K-major for the
-contiguous ones (`--sfa-major` forces one; the library takes both).
+The activation scales (SFA) are passed in the MN-major TMA-aligned layout the
+reference's kernels consume (K-major for the decode shape, where the two are
+equal; `--sfa-major` forces one; the library takes both).
 
 Each launch has 8 rotating buffer sets (copies of its inputs and outputs) and
 step s runs on set s % 8, so no launch finds its operands in L2 or the 256 MB
@@ -217,10 +217,8 @@ def _quant_b(n, k, gen, dev):
 #          per_token_cast_to_fp8_mn_major writes it in one pass;
 #   'k'    the K-major layout per_token_cast_to_fp8 returns;
 #   'auto' (default) per launch, the layout its kernel reads fastest: MN-major
-#          for the dense and masked kernels (3.5% and 6% faster than K-major), and
-#          K-major for the contiguous one, whose two-stage tiles fetch K-major
-#          scales four K blocks per request and keep the split stage hand-off only
-#          with them (MN-major is 2% slower there).
+#          for the dense, masked and contiguous kernels (3.5%, 6% and 3.5% faster
+#          than K-major), K-major for the decode shape (no difference).
 SFA_MAJOR = 'auto'
 
 
@@ -390,7 +388,7 @@ def make_contiguous():
     for op in ops['shapes']:
         n, k = op['n'], op['k']
 
-        def mk(a=_sfa(op['a'], 'k'), b=op['b'], n=n):
+        def mk(a=_sfa(op['a'], 'mn'), b=op['b'], n=n):
             a2, b2 = _twin(a), _twin(b)
             d2 = torch.empty((m_pad, n), dtype=torch.bfloat16, device=dev)
             return lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a2, b2, d2, idx)
@@ -399,7 +397,7 @@ def make_contiguous():
         launches.append(Launch(op['name'], mk, 2 * total * n * k, nbytes))
     cfg = {'workload': 'm_grouped_fp8_gemm_nt_contiguous 8 experts 32768 tokens Dirichlet(1)',
            'tokens_per_expert': ops['ms'], 'm_padded': m_pad, 'nk': [(4096, 7168), (7168, 2048)],
-           'sfa': _sfa_name('k')}
+           'sfa': _sfa_name('mn')}
     return launches, cfg
 
 
@@ -490,7 +488,7 @@ def make_moe_l1():
     m = masked_operands(dev)
     co, mo = c['shapes'][0], m['shapes'][0]
     assert (co['n'], co['k']) == (4096, 7168) and (mo['n'], mo['k']) == (4096, 7168)
-    co['a'], mo['a'] = _sfa(co['a'], 'k'), _sfa(mo['a'], 'mn')
+    co['a'], mo['a'] = _sfa(co['a'], 'mn'), _sfa(mo['a'], 'mn')
     n, k = co['n'], co['k']
     inter = n // 2
     m_pad, idx, total = c['m_pad'], c['m_indices'], c['total']

@@ -471,10 +471,9 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // hand-off: each hand-off then queues half the loads (a wave blocked on a
     // full load queue issues no MFMA either), and B gets most of two blocks to
     // land. At the hand-off the B side of stage kb + 2 (and the block's
-    // scale-group load) may stay in flight. (Persistent tiles, and contiguous
-    // ones without 4-block scale groups, keep the single hand-off: with the extra
-    // barrier they spill registers.)
-    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D && !PERSIST && (KIND != kContiguous || KSA == 4);
+    // scale-group load) may stay in flight. (Persistent tiles keep the single
+    // hand-off: with the extra barrier they spill registers.)
+    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D && !PERSIST;
     // The main loop's MFMA / promotion order: pinned (each sub-tile's MFMA pair,
     // then the previous sub-tile's FMAs) with masks that let LDS, vector-memory
     // and scalar instructions cross, rather than the compiler's interleaving.

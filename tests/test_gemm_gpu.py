@@ -228,6 +228,49 @@ def test_mn_major_sfa_equals_k_major(tile, m, n, k):
     assert diff < 1e-3
 
 
+@pytest.mark.parametrize('tile', [None, (2, 256, 256), (2, 256, 192)])
+@pytest.mark.parametrize('k', [1024, 1408, 2048])
+def test_contiguous_mn_major_sfa_equals_k_major(tile, k):
+    """m-grouped contiguous with MN-major SFA (per-stage scale loads and the split
+    stage hand-off) gives the bits of K-major SFA (4-block scale groups when
+    K % 512 == 0), with an empty expert and 256-row tiles that straddle two
+    experts (two passes), padding rows untouched."""
+    ms, n = [300, 0, 150, 420], 512
+    aligned = [(x + 127) // 128 * 128 for x in ms]
+    m_pad = sum(aligned)
+    layout_np = np.full(m_pad, -1, dtype=np.int32)
+    start = 0
+    for e, (mi, ai) in enumerate(zip(ms, aligned)):
+        layout_np[start:start + mi] = e
+        start += ai
+    dg = torch.Generator(device=DEV).manual_seed(43 + k)
+    a_bf = torch.randn((m_pad, k), generator=dg, device=DEV).bfloat16()
+    a_bf[torch.from_numpy(layout_np < 0).to(DEV)] = 0
+    aq, asf = deep_gemm.per_token_cast_to_fp8(a_bf, use_ue8m0=False)
+    asf_mn = deep_gemm.get_mn_major_tma_aligned_tensor(asf)
+    bq = torch.empty((len(ms), n, k), dtype=torch.float8_e4m3fn, device=DEV)
+    bs = torch.empty((len(ms), n // 128, (k + 127) // 128), device=DEV)
+    for e in range(len(ms)):
+        bq[e], bs[e] = deep_gemm.per_block_cast_to_fp8(torch.randn((n, k), generator=dg, device=DEV).bfloat16(),
+                                                       use_ue8m0=False)
+    layout = gen.to_dev(layout_np)
+    outs = []
+    if tile is not None:
+        deep_gemm.set_tile_override(tile[1], tile[2], variant=tile[0])
+    try:
+        for sf in (asf, asf_mn):
+            d = sentinel_bf16((m_pad, n))
+            deep_gemm.m_grouped_fp8_gemm_nt_contiguous((aq, sf), (bq, bs), d, layout)
+            print(f'contiguous sfa layouts k={k} tile={tile}: {deep_gemm.get_last_config()}', flush=True)
+            outs.append(d)
+    finally:
+        deep_gemm.set_tile_override(0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    pad = torch.from_numpy(layout_np < 0).to(DEV)
+    assert bool((outs[1].view(torch.int16)[pad] == SENTINEL).all())
+
+
 def test_k_zero_and_empty():
     m, n = 64, 128
     a = torch.empty((m, 0), dtype=torch.float8_e4m3fn, device=DEV)
