@@ -905,6 +905,30 @@ def test_persistent_equals_per_tile_launch(case):
     print(cfg_ref, '|', cfg, flush=True)
     assert 'v4' in cfg
     assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+    # and against the oracle: the rows the call writes, within one BF16 ulp plus the
+    # accumulation term; the rest keep the sentinel
+    if case in ('dense', 'dense_ragged'):
+        oref = ogemm.gemm_nt(oquant.dequant_per_token(x['qa'], x['sfa']), oquant.dequant_per_block(x['qb'], x['sfb']))
+        written = np.ones(oref.shape[0], dtype=bool)
+    else:
+        groups = x['qb'].shape[0]
+        b_deq = np.stack([oquant.dequant_per_block(x['qb'][i], x['sfb'][i]) for i in range(groups)])
+        if case == 'masked':
+            a_deq = np.stack([oquant.dequant_per_token(x['qa'][i], x['sfa'][i]) for i in range(groups)])
+            oref, written = ogemm.gemm_masked(a_deq, b_deq, x['masked_m'])
+        else:
+            a_deq = oquant.dequant_per_token(x['qa'], x['sfa'])
+            if case == 'contiguous':
+                oref, written = ogemm.gemm_contiguous(a_deq, b_deq, x['m_indices'])
+            else:
+                oref, written = ogemm.gemm_psum(a_deq, b_deq, ends, 256, 256, True)
+    out = got.float().cpu().numpy()
+    diff, _ = report(f'persistent {case} vs oracle', out[written], oref[written])
+    assert diff < 1e-3
+    k = x['qa'].shape[-1]
+    tol = np.abs(oref[written]) * 2.0 ** -8 + 2.0 ** -20 * np.sqrt(k) * np.abs(oref[written]).max()
+    assert np.all(np.abs(out[written] - oref[written]) <= tol)
+    assert bool((got.view(torch.int16)[torch.from_numpy(~written).to(DEV)] == SENTINEL).all())
 
 
 # ----------------------------------------------------------------- SF layouts
