@@ -234,7 +234,9 @@ def test_fused_config3_full_size():
     gl = gen.to_dev(m_idx)
     q, sf = _alloc_out((rows,), inter)
     deep_gemm.m_grouped_fp8_gemm_nt_contiguous_swiglu((qa, sfa), wf, (q, sf), gl, rw)
-    print(deep_gemm.get_last_config(), flush=True)
+    cfg = deep_gemm.get_last_config()
+    print(cfg, flush=True)
+    assert 'split_m=' in cfg   # the row split into 256 x 256 and 128 x 256 launches
     h = torch.empty((rows, 2 * inter), dtype=torch.bfloat16, device=DEV)
     deep_gemm.m_grouped_fp8_gemm_nt_contiguous((qa, sfa), (wq, ws), h, gl)
     rq, rsf = deep_gemm.moe_swiglu_apply_weight_to_fp8(h, rw, gl)
