@@ -931,6 +931,37 @@ def test_persistent_equals_per_tile_launch(case):
     assert bool((got.view(torch.int16)[torch.from_numpy(~written).to(DEV)] == SENTINEL).all())
 
 
+@pytest.mark.parametrize('expected_m,persistent', [(200, True), (1000, True), (1100, False)])
+def test_masked_routing_persistent_when_sparse(expected_m, persistent):
+    """Masked calls whose expected_m leaves at least half of max_m's 256-row blocks
+    empty run the persistent walk (variant 4) by default, otherwise one workgroup
+    per tile; either way the bits are those of the forced per-tile launch, and rows
+    past masked_m keep the sentinel. masked_m values far from expected_m (0, 1,
+    a whole group) only change the speed."""
+    print(f'masked routing expected_m={expected_m}', flush=True)
+    g, max_m, n, k = 5, 2048, 4096, 1024
+    x = gen.masked_inputs(g, max_m, n, k, seed=95)
+    x['masked_m'][:] = [0, 1, 300, 2048, 700]
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    mm = gen.to_dev(x['masked_m'])
+
+    def run():
+        d = sentinel_bf16((g, max_m, n))
+        deep_gemm.m_grouped_fp8_gemm_nt_masked(a, b, d, mm, expected_m=expected_m)
+        return d
+
+    deep_gemm.set_tile_override(0, 0)
+    got = run()
+    torch.cuda.synchronize()
+    cfg = deep_gemm.get_last_config()
+    ref, cfg_ref = _with_variant(2, run)
+    print(cfg, '|', cfg_ref, flush=True)
+    assert ('v4' in cfg) == persistent and 'block_m=256 block_n=256' in cfg
+    assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+    rows = torch.arange(max_m, device=DEV)[None, :] >= mm[:, None]
+    assert bool((got.view(torch.int16)[rows] == SENTINEL).all())
+
+
 # ----------------------------------------------------------------- SF layouts
 
 # the reference's grid (tests/generators.py:276-285, tests/test_layout.py:45-80), plus a ragged mn
