@@ -976,8 +976,9 @@ void swiglu_l1_impl(GemmKind kind, const dg_tensor* a_, const dg_tensor* sfa_, c
     args.sw_clamp = clamp > 0.f ? clamp : 0.f;
 
     // Tile: the 256-column tiles of the pipelined kernel (256 rows when K % 128 == 0
-    // and the layout allows, else 128), or for masked decode groups the
-    // weight-streaming kernel with 8 waves (256 columns).
+    // and the layout allows, else 128; for masked groups far below max_m the
+    // persistent 256 x 256 walk), or for masked decode groups the weight-streaming
+    // kernel with 8 waves (256 columns).
     const int tv = g_tile_variant.load(), tm = g_tile_m.load(), tn = g_tile_n.load();
     const bool ktail = k % 128 != 0;
     if (ceil_div(k, 128) > 1024) DG_UNSUPPORTED("fused SwiGLU: K up to 131072");
@@ -999,6 +1000,8 @@ void swiglu_l1_impl(GemmKind kind, const dg_tensor* a_, const dg_tensor* sfa_, c
         DG_UNSUPPORTED("tile override: the fused SwiGLU epilogue runs variants 2 and 5");
     } else if (stream_ok && expected_m <= kMaskedStreamRows) {
         t = {kMaskedStreamRows, 256, 5};
+    } else if (masked && t.block_m == 256 && ceil_div(m, 256) >= 2 * ceil_div(std::max(expected_m, 1), 256)) {
+        t.variant = 4;   // the persistent group walk, as for the plain masked launch (run_gemm)
     }
     if (t.variant == 2 && !grouped_tile_ok(kind, 2, t.block_m, align_m))
         DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 128 for the fused SwiGLU epilogue");

@@ -109,7 +109,7 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     constexpr bool SPLIT_SB = !SB1D && !(BN % 128 == 0 && WN <= 128 && 128 % WN == 0);
     static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
     static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
-    static_assert(!EPI || (BN == 256 && !PERSIST && !SB1D && !OUT_F32 && !HAS_C &&
+    static_assert(!EPI || (BN == 256 && (!PERSIST || KIND == kMasked) && !SB1D && !OUT_F32 && !HAS_C &&
                            (KIND == kContiguous || KIND == kMasked || KIND == kPsum) &&
                            STAGES * STAGE_BYTES >= SwigluTile<BM>::kBytes),
                   "SwiGLU epilogue: m-grouped 256-column tiles whose stage ring holds the BF16 tile");
@@ -787,8 +787,13 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
                                bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
     } while (0)
     if (a.sw_q) {   // fused SwiGLU -> FP8 epilogue (m-grouped 256-column tiles)
-        if constexpr (BN == 256 && !PERSIST && (KIND == kContiguous || KIND == kMasked || KIND == kPsum)) {
-            if (k_tail)
+        // (persistent: the masked group walk only)
+        if constexpr (BN == 256 && (PERSIST ? KIND == kMasked : (KIND == kContiguous || KIND == kMasked ||
+                                                                  KIND == kPsum))) {
+            if constexpr (PERSIST)   // (a 256 x 256 tile: no K tail; no K-major scale groups)
+                hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 0, 1, 0, 0, 1>),
+                                   gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);
+            else if (k_tail)
                 hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, KT_OK ? 1 : 0, 0, 0,
                                                               0, 1>),
                                    gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);

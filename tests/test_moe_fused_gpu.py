@@ -192,6 +192,34 @@ def test_fused_masked_equals_unfused(tile, masked_m):
     _check_rows(q, sf, rq.view(g, max_m, -1), rsf.view(g, max_m, -1), stored)
 
 
+@pytest.mark.parametrize('masked_m', [[0, 1, 300, 1024], [200, 513, 7, 256]])
+def test_fused_masked_sparse_persistent(masked_m):
+    """Masked groups far below max_m (expected_m 200 of 1024) run the persistent
+    group walk (variant 4) on the fused path too: the same bits as the unfused
+    pipeline, rows past masked_m untouched."""
+    g, max_m, inter, k = len(masked_m), 1024, 512, 1024
+    qa = np.empty((g, max_m, k), np.uint8)
+    sfa = np.empty((g, max_m, k // 128), np.float32)
+    for e in range(g):
+        qa[e], sfa[e] = oquant.per_token_cast_to_fp8(gen.randn_bf16((max_m, k), 60 + e), use_ue8m0=False)
+    a = (gen.to_dev(qa, torch.float8_e4m3fn), gen.to_dev(sfa))
+    w_std = _weights(g, 2 * inter, k, 70)
+    w_fused = deep_gemm.transform_l1_weights_for_swiglu(w_std)
+    rw = gen.to_dev(np.random.default_rng(8).random((g, max_m)).astype(np.float32))
+    mm = gen.to_dev(np.array(masked_m, np.int32))
+    q, sf = _alloc_out((g, max_m), inter)
+    deep_gemm.m_grouped_fp8_gemm_nt_masked_swiglu(a, w_fused, (q, sf), mm, expected_m=200, row_weights=rw)
+    cfg = deep_gemm.get_last_config()
+    h = torch.zeros((g, max_m, 2 * inter), dtype=torch.bfloat16, device=DEV)
+    deep_gemm.m_grouped_fp8_gemm_nt_masked(a, w_std, h, mm, expected_m=200)
+    rq, rsf = deep_gemm.moe_swiglu_apply_weight_to_fp8(h.view(g * max_m, -1), rw.view(-1))
+    torch.cuda.synchronize()
+    print(cfg, flush=True)
+    assert 'v4' in cfg
+    stored = (np.arange(max_m)[None, :] < np.array(masked_m)[:, None]).reshape(-1)
+    _check_rows(q, sf, rq.view(g, max_m, -1), rsf.view(g, max_m, -1), stored)
+
+
 def test_fused_reruns_bitwise():
     """The fused launches are deterministic: 10 reruns of each kernel give the same bytes."""
     ms = [500, 37, 260]
