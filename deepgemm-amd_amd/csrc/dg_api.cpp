@@ -623,6 +623,17 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
             if (kind == kMasked && tv == 0 && t.variant == 2 && t.block_m == 256 && t.block_n == 256 &&
                 ceil_div(m_rows, 256) >= 2 * ceil_div(std::max(expected_m, 1), 256))
                 t.variant = 4;
+            // Short K over many rounds of tiles (BF16 D, no C): the per-tile launch
+            // pays each workgroup's start and first-stage wait once per tile of a
+            // dozen K blocks, the persistent walk once per CU. Measured, per launch
+            // (MN-major / K-major SFA, µs): 4096 x 24576 x 1536 (6 rounds) 189.9 ->
+            // 184.5 / 195 -> 189; contiguous 33408 x 7168 x 2048 (14 rounds) 584 ->
+            // 566 / 600 -> 585. It loses at 1-2 rounds (4096 x 7168 x 2048 +4%), at
+            // K >= 7168 (+3-10%) and with FP32 C (4096 x 24576 x 1536 +1.5%).
+            if ((kind == kNormal || kind == kContiguous) && tv == 0 && t.variant == 2 && t.block_m == 256 &&
+                t.block_n == 256 && !args.out_f32 && args.c == nullptr && k <= 2048 &&
+                ceil_div(m_rows, 256) * ceil_div(n, 256) >= 4 * (int64_t)args.grid_limit)
+                t.variant = 4;
         }
         if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");

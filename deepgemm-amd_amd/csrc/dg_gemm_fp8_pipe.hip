@@ -481,9 +481,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // contiguous 1633-1639 against 1649-1657 us (with warm caches in a stripped
     // copy, 2-3% per shape); with masks that stop everything (0) it was 1-3%
     // slower than the compiler's order. 1D1D tiles keep the compiler's order
-    // (pinned, the K-grouped launch took 2117-2139 against 2073-2113 us), and so
-    // do persistent ones (not measured).
-    constexpr bool PIN_PROMO = !PERSIST && !SB1D;
+    // (pinned, the K-grouped launch took 2117-2139 against 2073-2113 us).
+    // Persistent tiles take it (config-2 shapes all as persistent launches: 945
+    // against 980 us; sparse masked groups 1-2% faster).
+    constexpr bool PIN_PROMO = !SB1D;
     constexpr int kPinMask = 0x7F4;   // SALU, VMEM, DS and transcendental may cross; VALU and MFMA may not
     auto wait_stage = [&](int s) {
         __builtin_amdgcn_sched_barrier(0);

@@ -962,6 +962,44 @@ def test_masked_routing_persistent_when_sparse(expected_m, persistent):
     assert bool((got.view(torch.int16)[rows] == SENTINEL).all())
 
 
+@pytest.mark.parametrize('case,k,persistent', [('dense', 1536, True), ('dense', 2176, False),
+                                               ('contiguous', 2048, True)])
+def test_short_k_many_rounds_routes_persistent(case, k, persistent):
+    """Dense and contiguous calls with K <= 2048 and at least four rounds of
+    256 x 256 tiles on the CUs (BF16 D, no C) run the persistent walk by default;
+    the bits are those of the forced per-tile launch."""
+    print(f'short-K routing {case} k={k}', flush=True)
+    if case == 'dense':
+        m, n = 4096, 16384   # 16 x 64 = 1024 tiles: four rounds on 256 CUs
+        x = gen.dense_inputs(m, n, k, seed=96)
+        a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+
+        def run():
+            d = sentinel_bf16((m, n))
+            deep_gemm.fp8_gemm_nt(a, b, d)
+            return d
+    else:
+        ms = [3000, 0, 5000, 129, 7000, 1200]
+        aligned = [(mi + 127) // 128 * 128 for mi in ms]
+        x = gen.contiguous_inputs(ms, aligned, 4096, k, seed=97)
+        a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+        mi_dev = gen.to_dev(x['m_indices'])
+
+        def run():
+            d = sentinel_bf16((sum(aligned), 4096))
+            deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, mi_dev)
+            return d
+    deep_gemm.set_tile_override(0, 0)
+    got = run()
+    torch.cuda.synchronize()
+    cfg = deep_gemm.get_last_config()
+    ref, cfg_ref = _with_variant(2, run)
+    print(cfg, '|', cfg_ref, flush=True)
+    if deep_gemm.get_num_sms() >= 256:
+        assert ('v4' in cfg) == persistent
+    assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+
+
 # ----------------------------------------------------------------- SF layouts
 
 # the reference's grid (tests/generators.py:276-285, tests/test_layout.py:45-80), plus a ragged mn
