@@ -394,8 +394,9 @@ int64_t dense_split_columns(int64_t m_rows, int64_t n, int64_t k, int cus) {
 // bitwise that of one launch. Returns r1 and the second launch's tile, or 0 when
 // the per-round cost model gains less than 5% or K is under 4096 (as for the
 // column split). With 256-column tiles only (the fused SwiGLU epilogue) the bar
-// is 3%: config 3's gate/up launch, 2096 tiles, splits into 2048 tiles of
-// 256 x 256 and 80 of 128 x 256 for a modelled 3.5% (measured 1097 -> 1083 us).
+// is 3%: config 3's gate/up launch, 2096 tiles, split into 2048 tiles of
+// 256 x 256 and 80 of 128 x 256 for a modelled 3.5% (measured 1097 -> 1083 us;
+// at four rounds or more such launches now run persistent instead).
 int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int align_m, TileConfig& hi_tile,
                               bool bn256_only = false) {
     if (k < 4096) return 0;
@@ -418,6 +419,16 @@ int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int
             if (cost < best - 1e-9) best = cost, best_r1 = mb1 * 256, hi_tile = TileConfig{p.bm, p.bn, 2};
         }
     return best < (bn256_only ? 0.97 : 0.95) * whole ? best_r1 : 0;
+}
+
+// Whether a dense or contiguous call on 256 x 256 tiles runs as persistent
+// workgroups (variant 4): BF16 D without C, at least four rounds of tiles on
+// the CUs, and for dense calls K <= 2048 (measurements in run_gemm).
+bool is_persistent_route(GemmKind kind, const TileConfig& t, const Fp8GemmArgs& args, int64_t m_rows, int64_t n,
+                         int64_t k) {
+    if (!(kind == kContiguous || (kind == kNormal && k <= 2048))) return false;
+    if (t.variant != 2 || t.block_m != 256 || t.block_n != 256 || args.out_f32 || args.c != nullptr) return false;
+    return ceil_div(m_rows, 256) * ceil_div(n, 256) >= 4 * (int64_t)args.grid_limit;
 }
 
 void record_config(const char* kernel, GemmKind kind, const TileConfig& t, int64_t m, int64_t n, int64_t k,
@@ -623,17 +634,16 @@ void run_gemm(GemmKind kind, const Operands& o, const Recipe& r, int64_t m, int6
             if (kind == kMasked && tv == 0 && t.variant == 2 && t.block_m == 256 && t.block_n == 256 &&
                 ceil_div(m_rows, 256) >= 2 * ceil_div(std::max(expected_m, 1), 256))
                 t.variant = 4;
-            // Short K over many rounds of tiles (BF16 D, no C): the per-tile launch
-            // pays each workgroup's start and first-stage wait once per tile of a
-            // dozen K blocks, the persistent walk once per CU. Measured, per launch
-            // (MN-major / K-major SFA, µs): 4096 x 24576 x 1536 (6 rounds) 189.9 ->
-            // 184.5 / 195 -> 189; contiguous 33408 x 7168 x 2048 (14 rounds) 584 ->
-            // 566 / 600 -> 585. It loses at 1-2 rounds (4096 x 7168 x 2048 +4%), at
-            // K >= 7168 (+3-10%) and with FP32 C (4096 x 24576 x 1536 +1.5%).
-            if ((kind == kNormal || kind == kContiguous) && tv == 0 && t.variant == 2 && t.block_m == 256 &&
-                t.block_n == 256 && !args.out_f32 && args.c == nullptr && k <= 2048 &&
-                ceil_div(m_rows, 256) * ceil_div(n, 256) >= 4 * (int64_t)args.grid_limit)
-                t.variant = 4;
+            // Many rounds of tiles (BF16 D, no C): the per-tile launch pays each
+            // workgroup's start and first-stage wait once per tile, the persistent
+            // walk once per CU. Measured per launch (µs, per tile -> persistent):
+            // 4096 x 24576 x 1536 (6 rounds) 170-173 -> 168-172 (K-major SFA 195 ->
+            // 189); contiguous 33408 x 7168 x 2048 (14 rounds) 522-524 -> 509-510,
+            // 33408 x 4096 x 7168 (8 rounds, per tile with the row split) 958-961 ->
+            // 942-943. Dense calls with longer K are even (within 1-2% at 4-8
+            // rounds) and keep the per-tile launch and its column split; at 1-3.5
+            // rounds it loses (4096 x 7168 x 2048 +5%), and with FP32 C it is even.
+            if (tv == 0 && is_persistent_route(kind, t, args, m_rows, n, k)) t.variant = 4;
         }
         if (!grouped_tile_ok(kind, t.variant, t.block_m, align_m))
             DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 64");
@@ -1013,6 +1023,8 @@ void swiglu_l1_impl(GemmKind kind, const dg_tensor* a_, const dg_tensor* sfa_, c
         t = {kMaskedStreamRows, 256, 5};
     } else if (masked && t.block_m == 256 && ceil_div(m, 256) >= 2 * ceil_div(std::max(expected_m, 1), 256)) {
         t.variant = 4;   // the persistent group walk, as for the plain masked launch (run_gemm)
+    } else if (kind == kContiguous && is_persistent_route(kind, t, args, m, n, k)) {
+        t.variant = 4;   // many rounds of tiles: persistent, as the plain contiguous launch (run_gemm)
     }
     if (t.variant == 2 && !grouped_tile_ok(kind, 2, t.block_m, align_m))
         DG_UNSUPPORTED("M alignment for contiguous layout must be a multiple of 128 for the fused SwiGLU epilogue");
@@ -1021,7 +1033,7 @@ void swiglu_l1_impl(GemmKind kind, const dg_tensor* a_, const dg_tensor* sfa_, c
         launch_fp8_gemm_masked_stream(args, 8, false, stream);
         return;
     }
-    if (kind == kContiguous && tv == 0 && t.block_m == 256) {
+    if (kind == kContiguous && tv == 0 && t.variant == 2 && t.block_m == 256) {
         // the row split of the plain contiguous launch, with a 256-column second tile
         TileConfig ht{};
         const int64_t r1 = contiguous_split_rows(m, n, k, args.grid_limit, align_m, ht, true);

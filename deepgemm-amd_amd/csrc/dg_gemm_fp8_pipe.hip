@@ -109,7 +109,8 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     constexpr bool SPLIT_SB = !SB1D && !(BN % 128 == 0 && WN <= 128 && 128 % WN == 0);
     static_assert(SA_ROWS_PER_WAVE <= 64, "SFA rows per wave");
     static_assert(STAGES >= 2 && (STAGES - 2) * LOADS_PER_STAGE < 64, "vmcnt range");
-    static_assert(!EPI || (BN == 256 && (!PERSIST || KIND == kMasked) && !SB1D && !OUT_F32 && !HAS_C &&
+    static_assert(!EPI || (BN == 256 && (!PERSIST || KIND == kMasked || KIND == kContiguous) && !SB1D && !OUT_F32 &&
+                           !HAS_C &&
                            (KIND == kContiguous || KIND == kMasked || KIND == kPsum) &&
                            STAGES * STAGE_BYTES >= SwigluTile<BM>::kBytes),
                   "SwiGLU epilogue: m-grouped 256-column tiles whose stage ring holds the BF16 tile");
@@ -471,9 +472,10 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // hand-off: each hand-off then queues half the loads (a wave blocked on a
     // full load queue issues no MFMA either), and B gets most of two blocks to
     // land. At the hand-off the B side of stage kb + 2 (and the block's
-    // scale-group load) may stay in flight. (Persistent tiles keep the single
-    // hand-off: with the extra barrier they spill registers.)
-    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D && !PERSIST;
+    // scale-group load) may stay in flight. Persistent tiles take it too
+    // (spill-free with the pinned promotion order below; config-2 shapes as
+    // persistent launches 875-880 against 893-899 us).
+    constexpr bool SPLIT = STAGES == 2 && !KT && !SB1D;
     // The main loop's MFMA / promotion order: pinned (each sub-tile's MFMA pair,
     // then the previous sub-tile's FMAs) with masks that let LDS, vector-memory
     // and scalar instructions cross, rather than the compiler's interleaving.
@@ -788,9 +790,8 @@ void launch_kind(const Fp8GemmArgs& a, hipStream_t stream) {
                                bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);                          \
     } while (0)
     if (a.sw_q) {   // fused SwiGLU -> FP8 epilogue (m-grouped 256-column tiles)
-        // (persistent: the masked group walk only)
-        if constexpr (BN == 256 && (PERSIST ? KIND == kMasked : (KIND == kContiguous || KIND == kMasked ||
-                                                                  KIND == kPsum))) {
+        // (persistent: masked and contiguous)
+        if constexpr (BN == 256 && (KIND == kContiguous || KIND == kMasked || (!PERSIST && KIND == kPsum))) {
             if constexpr (PERSIST)   // (a 256 x 256 tile: no K tail; no K-major scale groups)
                 hipLaunchKernelGGL((fp8_gemm_1d2d_pipe_kernel<BM, BN, WGM, WGN, STAGES, KIND, 0, 0, 0, 1, 0, 0, 1>),
                                    gdim, bdim, 0, stream, a, num_m_blocks, num_n_blocks, raster_gm);

@@ -344,17 +344,19 @@ def _contiguous_case(ms, aligned, n, k):
     assert torch.equal(d.view(torch.int16), first.view(torch.int16))
 
 
-@pytest.mark.parametrize('ms,mn_major', [(None, False), ([8000, 0, 16500, 8700], True)])
+@pytest.mark.parametrize('ms,mn_major', [(None, False), ([2000, 0, 4500, 2200], True)])
 def test_contiguous_row_split_equals_one_launch(ms, mn_major):
-    """m-grouped contiguous calls (K >= 4096) whose 256 x 256 tiles would leave the
-    last round mostly empty run as two launches (the first rows on 256 x 256 tiles,
-    the last M blocks on smaller ones): bitwise the single 256 x 256 launch, padding
-    rows untouched, and rows on both sides of the split against the oracle. Cases:
-    config 3's token count (8 experts, Dirichlet sizes, 131 M blocks) and a split
-    inside a segment after an empty expert, with MN-major SFA."""
+    """m-grouped contiguous calls (K >= 4096, fewer than four rounds of tiles)
+    whose 256 x 256 tiles would leave the last round mostly empty run as two
+    launches (the first rows on 256 x 256 tiles, the last M blocks on smaller
+    ones): bitwise the single 256 x 256 launch, padding rows untouched, and rows
+    on both sides of the split against the oracle. Cases: 8 experts with
+    Dirichlet sizes over 8192 tokens (35 M blocks, 2.2 rounds) and a split inside
+    a segment after an empty expert, with MN-major SFA. (At four rounds or more
+    the launch runs persistent, test_many_rounds_routes_persistent.)"""
     n, k = 4096, 4096
     if ms is None:
-        ms, aligned = gen.contiguous_sizes(8, 32768, seed=7)
+        ms, aligned = gen.contiguous_sizes(8, 8192, seed=7)
     else:
         aligned = [(x + 127) // 128 * 128 for x in ms]
     g, m_pad = len(ms), sum(aligned)
@@ -963,12 +965,12 @@ def test_masked_routing_persistent_when_sparse(expected_m, persistent):
 
 
 @pytest.mark.parametrize('case,k,persistent', [('dense', 1536, True), ('dense', 2176, False),
-                                               ('contiguous', 2048, True)])
-def test_short_k_many_rounds_routes_persistent(case, k, persistent):
-    """Dense and contiguous calls with K <= 2048 and at least four rounds of
-    256 x 256 tiles on the CUs (BF16 D, no C) run the persistent walk by default;
-    the bits are those of the forced per-tile launch."""
-    print(f'short-K routing {case} k={k}', flush=True)
+                                               ('contiguous', 2048, True), ('contiguous', 4096, True)])
+def test_many_rounds_routes_persistent(case, k, persistent):
+    """Contiguous calls, and dense calls with K <= 2048, with at least four rounds
+    of 256 x 256 tiles on the CUs (BF16 D, no C) run the persistent walk by
+    default; the bits are those of the forced per-tile launch."""
+    print(f'many-rounds routing {case} k={k}', flush=True)
     if case == 'dense':
         m, n = 4096, 16384   # 16 x 64 = 1024 tiles: four rounds on 256 CUs
         x = gen.dense_inputs(m, n, k, seed=96)

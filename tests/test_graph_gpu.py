@@ -125,7 +125,7 @@ def test_graph_split_calls():
     replay_matches_eager(lambda: deep_gemm.fp8_gemm_nt(a, b, d), d)
     assert 'split_n=' in deep_gemm.get_last_config()
 
-    ms, aligned = gen.contiguous_sizes(8, 32768, seed=7)   # 33408 rows: 131 M blocks
+    ms, aligned = gen.contiguous_sizes(8, 8192, seed=7)   # 8832 rows: 35 M blocks, 2.2 rounds
     n, k = 4096, 4096
     m_pad = sum(aligned)
     layout_np = np.full(m_pad, -1, dtype=np.int32)
@@ -145,3 +145,17 @@ def test_graph_split_calls():
     replay_matches_eager(lambda: deep_gemm.m_grouped_fp8_gemm_nt_contiguous(ca, (bq, bs), dc, layout), dc,
                          written=torch.from_numpy(layout_np >= 0).to(DEV))
     assert 'split_m=' in deep_gemm.get_last_config()
+
+
+def test_graph_persistent_call():
+    """A call routed to persistent workgroups (config 2's 4096 x 24576 x 1536: six
+    rounds of tiles) captures and replays bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(10)
+    m, n, k = 4096, 24576, 1536
+    a = deep_gemm.per_token_cast_to_fp8(torch.randn((m, k), generator=g, device=DEV).bfloat16(), use_ue8m0=False)
+    b = deep_gemm.per_block_cast_to_fp8(torch.randn((n, k), generator=g, device=DEV).bfloat16(), use_ue8m0=False)
+    d = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    print('graph persistent 4096x24576x1536', flush=True)
+    replay_matches_eager(lambda: deep_gemm.fp8_gemm_nt(a, b, d), d)
+    if deep_gemm.get_num_sms() >= 256:
+        assert ' v4 ' in deep_gemm.get_last_config()

@@ -264,7 +264,7 @@ def test_fused_config3_full_size():
     deep_gemm.m_grouped_fp8_gemm_nt_contiguous_swiglu((qa, sfa), wf, (q, sf), gl, rw)
     cfg = deep_gemm.get_last_config()
     print(cfg, flush=True)
-    assert 'split_m=' in cfg   # the row split into 256 x 256 and 128 x 256 launches
+    assert 'v4' in cfg   # eight rounds of 256 x 256 tiles: persistent workgroups
     h = torch.empty((rows, 2 * inter), dtype=torch.bfloat16, device=DEV)
     deep_gemm.m_grouped_fp8_gemm_nt_contiguous((qa, sfa), (wq, ws), h, gl)
     rq, rsf = deep_gemm.moe_swiglu_apply_weight_to_fp8(h, rw, gl)
