@@ -40,13 +40,15 @@ def _x(t, kdim, seed):
 
 @pytest.mark.parametrize('layout', ['contiguous', 'psum', 'masked'])
 @pytest.mark.parametrize('t,k,e,kdim', [(1, 1, 4, 256), (100, 2, 8, 512), (1000, 8, 32, 1024), (300, 6, 256, 256),
-                                         (20000, 2, 1024, 128), (70, 3, 5, 8320)])
+                                         (4096, 8, 256, 512), (1024, 2, 1024, 128), (1025, 2, 1024, 128),
+                                         (5000, 4, 64, 256), (20000, 2, 1024, 128), (70, 3, 5, 8320)])
 def test_dispatch_vs_oracle(layout, t, k, e, kdim):
-    """Dispatch against the oracle in all three layouts. The last two cases cover
-    the kernels' multi-round paths: 313 chunks of 64 tokens (the per-expert
-    scan's 256-chunk rounds) over 1024 experts (every id bit in the ballot
-    ranking), and rows of 8320 bytes with 65 scales (two 8 KB copy rounds, two
-    64-scale rounds)."""
+    """Dispatch against the oracle in all three layouts, from one token to
+    config-scale calls (4096 tokens, top-8 over 256 experts). The last two cases
+    cover the kernels' multi-round paths: 313 chunks of 64 tokens (the
+    per-expert scan's 256-chunk rounds) over 1024 experts (every id bit in the
+    ballot ranking), and rows of 8320 bytes with 65 scales (two 8 KB copy
+    rounds, two 64-scale rounds)."""
     idx, w = _routing(t, k, e, seed=t + k + e)
     q, sf = _x(t, kdim, seed=t)
     max_m = 64 if layout == 'masked' else 0          # small enough that some experts overflow
