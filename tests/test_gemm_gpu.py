@@ -1002,6 +1002,49 @@ def test_many_rounds_routes_persistent(case, k, persistent):
     assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
 
 
+@pytest.mark.parametrize('num_sms', [48, 7])
+def test_persistent_routes_with_fewer_cus(num_sms):
+    """With set_num_sms below the chip's CU count the persistent launches run that
+    many workgroups (each walks more tiles), and the four-round rule counts
+    rounds on that many CUs: contiguous and sparse masked calls give the bits of
+    the per-tile launch."""
+    old = deep_gemm.get_num_sms()
+    print(f'persistent with num_sms={num_sms}', flush=True)
+    ms = [1500, 0, 1800, 129, 900]   # 19 M blocks x 16 N blocks: >= 4 rounds on 48 CUs
+    aligned = [(mi + 127) // 128 * 128 for mi in ms]
+    x = gen.contiguous_inputs(ms, aligned, 4096, 1024, seed=98)
+    a, b = (e4m3(x['qa']), f32(x['sfa'])), (e4m3(x['qb']), f32(x['sfb']))
+    mi_dev = gen.to_dev(x['m_indices'])
+    xm = gen.masked_inputs(4, 1024, 2048, 1024, seed=99)
+    xm['masked_m'][:] = [0, 1, 256, 300]
+    am, bm = (e4m3(xm['qa']), f32(xm['sfa'])), (e4m3(xm['qb']), f32(xm['sfb']))
+    mm = gen.to_dev(xm['masked_m'])
+
+    def run_c():
+        d = sentinel_bf16((sum(aligned), 4096))
+        deep_gemm.m_grouped_fp8_gemm_nt_contiguous(a, b, d, mi_dev)
+        return d
+
+    def run_m():
+        d = sentinel_bf16((4, 1024, 2048))
+        deep_gemm.m_grouped_fp8_gemm_nt_masked(am, bm, d, mm, expected_m=200)
+        return d
+
+    try:
+        deep_gemm.set_num_sms(num_sms)
+        for run in (run_c, run_m):
+            deep_gemm.set_tile_override(0, 0)
+            got = run()
+            torch.cuda.synchronize()
+            cfg = deep_gemm.get_last_config()
+            ref, cfg_ref = _with_variant(2, run)
+            print(cfg, '|', cfg_ref, flush=True)
+            assert ' v4 ' in cfg
+            assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
+    finally:
+        deep_gemm.set_num_sms(old)
+
+
 # ----------------------------------------------------------------- SF layouts
 
 # the reference's grid (tests/generators.py:276-285, tests/test_layout.py:45-80), plus a ragged mn
