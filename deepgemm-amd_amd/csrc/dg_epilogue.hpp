@@ -23,6 +23,11 @@
 namespace dgm {
 namespace dev {
 
+// Default hook of RowEpilogue::run: nothing.
+struct NoEpilogueHook {
+    __device__ void operator()() const {}
+};
+
 template <int KIND, int OUT_F32, int HAS_C, int SM, int SN>
 struct RowEpilogue {
     static constexpr int WM = SM * 32, WN = SN * 32;
@@ -55,11 +60,14 @@ struct RowEpilogue {
     // fin: the wave's accumulators. region: the wave's LDS region (RPP rows).
     // row0 / col0: output coordinates of the wave's first row / column.
     // Rows outside [m_lo, m_hi) are neither stored nor zeroed.
-    template <int RPP>
+    // hook: called once the first pass is staged and the row flags are known
+    // (their index loads have returned); the pipelined kernel issues the next
+    // tile's first loads there.
+    template <int RPP, typename Hook = NoEpilogueHook>
     __device__ static void run(const f32x16 (&fin)[SM][SN], uint8_t* region, int lane, const Tile& t, int m_total,
                                const int32_t* __restrict__ layout, int row0, int col0, int n_total, int m_lo,
                                int m_hi, void* __restrict__ d, const void* __restrict__ c, int64_t ldd, int64_t ldc,
-                               int64_t d_goff) {
+                               int64_t d_goff, Hook&& hook = Hook{}) {
         static_assert(RPP % 32 == 0 && RPP > 0 && WM % RPP == 0, "rows per pass");
         // (opaque copy of the lane id: the kernels that run two passes inline
         // this twice, and values shared between the copies would stay live
@@ -74,7 +82,7 @@ struct RowEpilogue {
         for (int h = 0; h < NMASK; ++h) {
             const int m = row0 + h * 64 + lane;
             bool st = false, z = false;
-            if (h * 64 + lane < WM) row_predicate<KIND>(t, m_total, layout, m, st, z);
+            if (WM % 64 == 0 || h * 64 + lane < WM) row_predicate<KIND>(t, m_total, layout, m, st, z);
             if (m < m_lo || m >= m_hi) st = z = false;
             smask[h] = __ballot(st);
             zmask[h] = __ballot(z);
@@ -139,6 +147,17 @@ struct RowEpilogue {
                     }
             }
             if constexpr (HAS_C) prefetch_c(p0 / RPP);
+            if constexpr (!std::is_same_v<std::decay_t<Hook>, NoEpilogueHook>) {
+                // After the first pass is staged (the row flags' index loads return
+                // meanwhile) and before anything is read back. The flags stay ahead of
+                // the hook: the compiler does not count the hook's asm loads, so a
+                // flag computed after them would wait for them too.
+                if (p0 == 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    hook();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
             // ---- LDS -> global, one row segment of VPL outputs per lane
             // (LDS operations of one wave complete in order, so the reads see the
             // writes above and the next pass's writes follow these reads.)

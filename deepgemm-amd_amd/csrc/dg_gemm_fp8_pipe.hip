@@ -123,6 +123,17 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     __shared__ int s_flag;
     __shared__ int s_half_valid[2];
 
+    // PF: persistent two-stage launches issue the next tile's SFB and first stage
+    // into stage slot 0 during this tile's epilogue, which then stages its outputs
+    // in slot 1 only. pf_issued: the current tile's first pass finds them issued.
+    // Measured (interleaved runs on two boxes, per launch): 4096 x 24576 x 1536
+    // 171.8-175.1 -> 167.0-172.5 us. Contiguous launches showed no gain in the
+    // same runs (33408 x 7168 x 2048 within their +-10 us), so they keep the
+    // plain prologue.
+    constexpr bool PF = PERSIST && STAGES == 2 && !EPI && !KT && !SB1D && !KSA && !OUT_F32 && !HAS_C &&
+                        (KIND == kNormal || KIND == kMasked);
+    bool pf_issued = false;
+
     const int slot = xcd_remap(blockIdx.x, gridDim.x);
     for (int lt = slot;; lt += gridDim.x) {
     // Persistent: per-tile copies of the arguments and the lane id, re-read each
@@ -140,6 +151,14 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
         t = decode_tile_persistent<BM, BN, KIND, NT>(lt, p.m, p.n, p.num_groups, p.layout, p.align_m, p.zero_padding,
                                                      num_m_blocks, num_n_blocks, static_cast<uint16_t*>(p.d), p.ldd,
                                                      &s_flag, raster_gm);
+        if constexpr (PF) {
+            // (a tile is only prefetched when it exists and has rows; were that
+            // ever wrong, its loads are drained here rather than left writing LDS)
+            if (pf_issued && (t.done || !t.active)) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                pf_issued = false;
+            }
+        }
         if (t.done) break;
         if (!t.active) continue;
     } else {
@@ -210,11 +229,29 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     const int num_kb = (kdim + kBK - 1) / kBK;
     const int my_group = ((n0 & 127) + wn * WN) >> 7;
 
+    // The SFB rows of a tile (at most two 128-row groups of expert `e` from
+    // column n0x) straight into s_sfb, 64 K blocks per wave load.
+    auto issue_sfb = [&](int e, int n0x) {
+        const float* sfb_g = p.sfb + (int64_t)e * p.sfb_gs;
+        const int last_row = (p.n - 1) >> 7;
+        const uint32_t sfb_lds =
+            __builtin_amdgcn_readfirstlane(lds_address(reinterpret_cast<const uint8_t*>(&s_sfb[0][0])));
+        const int segs = (num_kb + 63) / 64;
+        for (int i = wave; i < 2 * segs; i += NW) {
+            const int gsel = i / segs, kb = (i % segs) * 64 + lane;
+            const int row = min((n0x >> 7) + gsel, last_row);
+            const float* src = sfb_g + (int64_t)row * p.sfb_sn + (int64_t)min(kb, num_kb - 1) * p.sfb_sk;
+            dma4_vaddr(src, sfb_lds + (uint32_t)(gsel * (int)sizeof(s_sfb[0]) + (i % segs) * 256));
+        }
+    };
+
     // One pass of the tile: the whole K loop and the epilogue. Written as a lambda
     // called once (twice only for split contiguous tiles), since a loop around
     // it costs registers even when it runs once.
     auto run_pass = [&](const int pass) {
     const int expert = pass_expert[pass];
+    // the pass's SFB and first stage were issued during the previous tile's epilogue
+    const bool pf_head = PF && pass == 0 && pf_issued;
     // In a masked group with few rows, a wave whose rows all lie past them only
     // loads and synchronizes. (`p.m >= 0` always holds; keeping the condition a
     // run-time value stops the compiler from moving promotion code across the
@@ -236,19 +273,8 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     // the first stages' instead of preceding it. (Loaded through registers, a
     // barrier had to separate them from the stage loads: config-2 step 869-876
     // against 879-881 us, interleaved runs.)
-    if constexpr (!SB1D) {
-        const float* sfb_g = p.sfb + (int64_t)expert * p.sfb_gs;
-        const int last_row = (p.n - 1) >> 7;
-        const uint32_t sfb_lds =
-            __builtin_amdgcn_readfirstlane(lds_address(reinterpret_cast<const uint8_t*>(&s_sfb[0][0])));
-        const int segs = (num_kb + 63) / 64;
-        for (int i = wave; i < 2 * segs; i += NW) {
-            const int gsel = i / segs, kb = (i % segs) * 64 + lane;
-            const int row = min((n0 >> 7) + gsel, last_row);
-            const float* src = sfb_g + (int64_t)row * p.sfb_sn + (int64_t)min(kb, num_kb - 1) * p.sfb_sk;
-            dma4_vaddr(src, sfb_lds + (uint32_t)(gsel * (int)sizeof(s_sfb[0]) + (i % segs) * 256));
-        }
-    }
+    if constexpr (!SB1D)
+        if (!pf_head) issue_sfb(expert, n0);
 
     const int lrow = lane & 31;
     const int lhalf = lane >> 5;
@@ -512,9 +538,12 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
     }
 #pragma unroll
     for (int s = 0; s < STAGES; ++s)
-        if (s < num_kb) issue_stage(s, s);
+        if (s < num_kb && !(s == 0 && pf_head)) issue_stage(s, s);
+    if constexpr (PF) pf_issued = false;
     __builtin_amdgcn_sched_barrier(0);
-    // (KSA: the group loads are in flight too; wait for all)
+    // (KSA: the group loads are in flight too; wait for all. PF: the prefetched
+    // stage 0 was issued before this tile's epilogue stores and stage 1; vector
+    // loads return in order, so the same count covers it.)
     if (!KSA && num_kb >= STAGES)
         wait_vmcnt_barrier<(STAGES - 1) * LOADS_PER_STAGE>();
     else
@@ -683,6 +712,16 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
             }
         }
     }
+    // PF: the next tile's coordinates (the dense and masked walks give every
+    // tile rows to compute), decoded here so that the masked walk's masked_m
+    // loads overlap the waits below.
+    PTile nx{};
+    bool pf_go = false;
+    if constexpr (PF) {
+        nx = persistent_tile_coords<BM, BN, KIND>(lt + (int)gridDim.x, p.m, p.num_groups, p.layout, num_m_blocks,
+                                                  num_n_blocks, raster_gm);
+        pf_go = !nx.done && num_kb > 0;
+    }
     // No stage load may still be writing LDS when the workgroup ends (or the
     // epilogue reuses it).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -715,15 +754,48 @@ fp8_gemm_1d2d_pipe_kernel(const Fp8GemmArgs p_arg, const int num_m_blocks, const
                               });
     } else {
         using Epi = RowEpilogue<KIND, OUT_F32, HAS_C, SM, SN>;
-        constexpr int REGION = (STAGES * STAGE_BYTES / NW) / 16 * 16;
+        // (PF: slot 0 receives the next tile's loads; the epilogue keeps to slot 1)
+        constexpr int REGION = PF ? (STAGE_BYTES / NW) / 16 * 16 : (STAGES * STAGE_BYTES / NW) / 16 * 16;
+        uint8_t* const region = smem + (PF ? STAGE_BYTES : 0) + wave * REGION;
         const int64_t d_goff = (KIND == kMasked || KIND == kKGrouped) ? (int64_t)t.g * p.d_gs : 0;
         const void* c_g = (KIND == kKGrouped && HAS_C) ? (const void*)(static_cast<const float*>(p.c) + (int64_t)t.g * p.c_gs)
                                                        : p.c;
         const int m_lo = npass == 2 ? m0 + pass * 128 : m0;
         const int m_hi = npass == 2 ? m_lo + 128 : m0 + BM;
-        Epi::template run<Epi::rows_per_pass(REGION)>(fin, smem + wave * REGION, lane, t, p.m, p.layout,
-                                                      m0 + wm * WM, n0 + wn * WN, p.n, m_lo, m_hi, p.d, c_g, p.ldd,
-                                                      p.ldc, d_goff);
+        if constexpr (PF) {
+            // The next tile's SFB and stage 0 (into slot 0, as its prologue would
+            // issue them), issued once the first rows are staged: they arrive while
+            // this tile's outputs are read back and stored.
+            auto prefetch_next = [&]() {
+                if (!pf_go) return;
+                const uint8_t* a2 = p.a + (KIND == kMasked ? (int64_t)nx.g * p.a_gs : 0) + (int64_t)nx.m0 * lda;
+                const uint8_t* b2 = p.b + (int64_t)nx.expert * p.b_gs + (int64_t)nx.n0 * ldb;
+                const float* sa2 = p.sfa + (KIND == kMasked ? (int64_t)nx.g * p.sfa_gs : 0) +
+                                   (int64_t)nx.m0 * p.sfa_sm;
+                const int a_rows2 = min(BM, nx.row_end - nx.m0), b_rows2 = min(BN, p.n - nx.n0);
+                issue_sfb(nx.expert, nx.n0);
+#pragma unroll
+                for (int i = 0; i < A_INSTR; ++i) {
+                    const int seg = i * NW + wave;
+                    seg_load(a2, seg, a_rows2, lda, vlane_a, smem_lds + seg * 1024);
+                }
+#pragma unroll
+                for (int i = 0; i < B_INSTR; ++i) {
+                    const int seg = i * NW + wave;
+                    seg_load(b2, seg, b_rows2, ldb, vlane_b, smem_lds + BM * kBK + seg * 1024);
+                }
+                dma4_saddr(reinterpret_cast<const uint8_t*>(sa2), (uint32_t)(min(sa_row, a_rows2 - 1) * p.sfa_sm) * 4u,
+                           smem_lds + SA_OFF + wave * 256);
+                pf_issued = true;
+            };
+            Epi::template run<Epi::rows_per_pass(REGION)>(fin, region, lane, t, p.m, p.layout, m0 + wm * WM,
+                                                          n0 + wn * WN, p.n, m_lo, m_hi, p.d, c_g, p.ldd, p.ldc,
+                                                          d_goff, prefetch_next);
+        } else {
+            Epi::template run<Epi::rows_per_pass(REGION)>(fin, region, lane, t, p.m, p.layout, m0 + wm * WM,
+                                                          n0 + wn * WN, p.n, m_lo, m_hi, p.d, c_g, p.ldd, p.ldc,
+                                                          d_goff);
+        }
     }
     };   // run_pass
 

@@ -190,11 +190,13 @@ struct PTile : Tile {
     int done;
 };
 
-template <int BM, int BN, int KIND, int NT>
-__device__ __forceinline__ PTile decode_tile_persistent(int lt, int m, int n, int num_groups,
-                                                        const int32_t* __restrict__ layout, int align_m,
-                                                        int zero_padding, int num_m_blocks, int num_n_blocks,
-                                                        uint16_t* zero_d, int64_t ldd, int* s_flag, int raster_gm) {
+// The coordinates part of decode_tile_persistent (group, m0, n0, row_end; done
+// past the end), without the per-row work: it reads nothing but masked_m, so a
+// kernel can also use it to look one tile ahead.
+template <int BM, int BN, int KIND>
+__device__ __forceinline__ PTile persistent_tile_coords(int lt, int m, int num_groups,
+                                                        const int32_t* __restrict__ layout, int num_m_blocks,
+                                                        int num_n_blocks, int raster_gm) {
     PTile t{};
     t.done = 0;
     int tile = lt;
@@ -230,7 +232,18 @@ __device__ __forceinline__ PTile decode_tile_persistent(int lt, int m, int n, in
     if constexpr (KIND == kMasked) {
         t.row_end = min(m, max(layout[t.g], 0));
         t.expert = t.g;
-    } else if constexpr (KIND == kContiguous) {
+    }
+    return t;
+}
+
+template <int BM, int BN, int KIND, int NT>
+__device__ __forceinline__ PTile decode_tile_persistent(int lt, int m, int n, int num_groups,
+                                                        const int32_t* __restrict__ layout, int align_m,
+                                                        int zero_padding, int num_m_blocks, int num_n_blocks,
+                                                        uint16_t* zero_d, int64_t ldd, int* s_flag, int raster_gm) {
+    PTile t = persistent_tile_coords<BM, BN, KIND>(lt, m, num_groups, layout, num_m_blocks, num_n_blocks, raster_gm);
+    if (t.done) return t;
+    if constexpr (KIND == kContiguous) {
         t.expert = min(max(0, layout[t.m0]), num_groups - 1);
         if (threadIdx.x == 0) *s_flag = 0;
         __syncthreads();
@@ -278,7 +291,10 @@ __device__ __forceinline__ void row_predicate(const Tile& t, int m, const int32_
     } else if constexpr (KIND == kMasked) {
         store = mrow < t.row_end;
     } else if constexpr (KIND == kContiguous) {
-        store = mrow < m && layout[mrow] >= 0;
+        // (the index load is unconditional, at a row clamped into [0, m), so that
+        // the loads of several rows can be in flight together)
+        const int id = layout[min(mrow, m - 1)];
+        store = mrow < m && id >= 0;
     } else {
         store = mrow < t.row_end;
         zero = !store && mrow < t.pad_end;

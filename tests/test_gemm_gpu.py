@@ -969,7 +969,9 @@ def test_masked_routing_persistent_when_sparse(expected_m, persistent):
 def test_many_rounds_routes_persistent(case, k, persistent):
     """Contiguous calls, and dense calls with K <= 2048, with at least four rounds
     of 256 x 256 tiles on the CUs (BF16 D, no C) run the persistent walk by
-    default; the bits are those of the forced per-tile launch."""
+    default; the bits are those of the forced per-tile launch. The contiguous
+    K = 4096 call (66 M blocks: 4.1 rounds) also takes the row split, its first
+    64 M blocks persistent and the last rows on smaller tiles."""
     print(f'many-rounds routing {case} k={k}', flush=True)
     if case == 'dense':
         m, n = 4096, 16384   # 16 x 64 = 1024 tiles: four rounds on 256 CUs
@@ -999,6 +1001,7 @@ def test_many_rounds_routes_persistent(case, k, persistent):
     print(cfg, '|', cfg_ref, flush=True)
     if deep_gemm.get_num_sms() >= 256:
         assert ('v4' in cfg) == persistent
+        assert ('split_m=16384:' in cfg) == (case == 'contiguous' and k == 4096), cfg
     assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
 
 
