@@ -396,8 +396,8 @@ int64_t dense_split_columns(int64_t m_rows, int64_t n, int64_t k, int cus) {
 // column split). With 256-column tiles only (the fused SwiGLU epilogue) the bar
 // is 3%: config 3's gate/up launch, 2096 tiles, split into 2048 tiles of
 // 256 x 256 and 80 of 128 x 256 for a modelled 3.5% (measured 1097 -> 1083 us).
-// Launches of four rounds or more take the persistent walk instead
-// (is_persistent_route), which measured faster still.
+// In launches of four rounds or more the first part takes the persistent walk
+// (is_persistent_route) when it still makes four rounds.
 int64_t contiguous_split_rows(int64_t m_rows, int64_t n, int64_t k, int cus, int align_m, TileConfig& hi_tile,
                               bool bn256_only = false) {
     if (k < 4096) return 0;

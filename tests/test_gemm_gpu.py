@@ -346,14 +346,14 @@ def _contiguous_case(ms, aligned, n, k):
 
 @pytest.mark.parametrize('ms,mn_major', [(None, False), ([2000, 0, 4500, 2200], True)])
 def test_contiguous_row_split_equals_one_launch(ms, mn_major):
-    """m-grouped contiguous calls (K >= 4096, fewer than four rounds of tiles)
+    """m-grouped contiguous calls (K >= 4096; here fewer than four rounds of tiles)
     whose 256 x 256 tiles would leave the last round mostly empty run as two
     launches (the first rows on 256 x 256 tiles, the last M blocks on smaller
     ones): bitwise the single 256 x 256 launch, padding rows untouched, and rows
     on both sides of the split against the oracle. Cases: 8 experts with
     Dirichlet sizes over 8192 tokens (35 M blocks, 2.2 rounds) and a split inside
     a segment after an empty expert, with MN-major SFA. (At four rounds or more
-    the launch runs persistent, test_many_rounds_routes_persistent.)"""
+    the first part runs persistent, test_many_rounds_routes_persistent.)"""
     n, k = 4096, 4096
     if ms is None:
         ms, aligned = gen.contiguous_sizes(8, 8192, seed=7)
