@@ -840,12 +840,16 @@ def _with_variant(v, fn):
         deep_gemm.set_tile_override(0, 0)
 
 
+@pytest.mark.parametrize('num_sms', [0, 7])
 @pytest.mark.parametrize('case', ['dense', 'dense_ragged', 'contiguous', 'masked', 'psum'])
-def test_persistent_equals_per_tile_launch(case):
+def test_persistent_equals_per_tile_launch(case, num_sms):
     """The persistent scheduler (grid = CU count, tile stride = grid, masked and
     psum group walks) gives the same bits as one workgroup per tile: same tile
-    shape, same per-output K order; rows it must not touch stay untouched."""
-    print(f'persistent {case}', flush=True)
+    shape, same per-output K order; rows it must not touch stay untouched. With
+    num_sms = 7 every workgroup walks several tiles, so the dense and masked
+    walks also issue each next tile's first stage during the epilogue (ragged
+    M and N edges and one-row groups included)."""
+    print(f'persistent {case} num_sms={num_sms or "all"}', flush=True)
     if case in ('dense', 'dense_ragged'):
         m, n, k = (1024, 2048, 1024) if case == "dense" else (1300, 712, 896)
         x = gen.dense_inputs(m, n, k, seed=91)
@@ -897,13 +901,17 @@ def test_persistent_equals_per_tile_launch(case):
                                                        ensure_zero_padding=True)
             return d
     old_align = deep_gemm.get_mk_alignment_for_contiguous_layout()
+    old_sms = deep_gemm.get_num_sms()
     if case == 'psum':
         deep_gemm.set_mk_alignment_for_contiguous_layout(256)
     try:
+        if num_sms:
+            deep_gemm.set_num_sms(num_sms)
         ref, cfg_ref = _with_variant(2, run)
         got, cfg = _with_variant(4, run)
     finally:
         deep_gemm.set_mk_alignment_for_contiguous_layout(old_align)
+        deep_gemm.set_num_sms(old_sms)
     print(cfg_ref, '|', cfg, flush=True)
     assert 'v4' in cfg
     assert torch.equal(ref.view(torch.int16), got.view(torch.int16))
